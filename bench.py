@@ -1,0 +1,295 @@
+#!/usr/bin/env python3
+"""Driver benchmark: one JSON line for the kernel-registry hot path on MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+A "step" is one dispatch of a registry entry over one batch of synthetic,
+seeded input already resident in HBM.  The headline workload is the LLaMA
+decoder decode step ("decoder block us/step"); the other four
+configurations (sqr_mm, transpose_2d, conv2d, large_mm) are timed the same way
+and reported under "kernels", each with its own roofline fraction.
+
+Timing: W untimed steps, then exactly K steps launched back to back through
+mb_run (a hipEvent pair per step on the library stream), bracketed by
+torch.cuda.synchronize() on both sides; ms_per_step is the host wall clock of
+the K steps / K.  `roofline.achieved` is the algorithmic bytes (HBM-bound
+kernels) or flops (MFMA-bound kernels) of ONE launch of the dominant kernel
+divided by that kernel's mean event-timed duration over the same K steps.
+
+cpu_baseline: the float64 numpy oracle (oracle/), timed on this host on a
+bounded sample of the same workload — a reported baseline, not a target.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+METRIC = "TFLOP/s or GB/s as % of MI355X roofline per kernel; decoder block µs/step"
+HBM_PEAK_GBPS = 8000.0
+MFMA_PEAK_TFLOPS = {"f32": 157.3, "bf16": 2516.6}
+
+# Decoder decode-step shapes (registry mlx/kernels/full/registry.py).
+_B, _D, _H, _HKV, _DH, _FF, _L = 16, 4096, 32, 8, 128, 14336, 2048
+
+
+def _decoder_part_bytes() -> dict:
+    """Algorithmic HBM bytes of one launch of each decoder kernel: every weight
+    and cache byte once, activations in and out once (bf16 = 2 bytes)."""
+    qkv_n = _D + 2 * _HKV * _DH
+    return {
+        "qkv_rope": 2 * (_D * qkv_n + _B * _D + _B * _D + 2 * _B * _HKV * _DH),
+        "attention": 2 * (2 * _B * _HKV * _L * _DH + _B * _D),
+        "wo_residual": 2 * (_D * _D + 2 * _B * _D) + 4 * _B * _D,
+        "gate_up_swiglu": 2 * (_D * 2 * _FF + _B * _D + _B * _FF),
+        "down_residual": 2 * (_FF * _D + _B * _FF + _B * _D) + 4 * _B * _D,
+    }
+
+
+# Per workload: (dominant part name or None for single-kernel, bound, units of
+# algorithmic work per launch, unit of `value`).
+def _work(name: str, meta: dict):
+    if name == "llama_decoder_step":
+        parts = _decoder_part_bytes()
+        return dict(part="gate_up_swiglu", bound="hbm", per_launch=parts["gate_up_swiglu"],
+                    parts=parts)
+    if meta.get("flops", 0) == 0:
+        return dict(part=None, bound="hbm", per_launch=int(meta["bytes"]))
+    return dict(part=None, bound="mfma", per_launch=int(meta["flops"]))
+
+
+def _value_unit(name: str, meta: dict, ms_per_step: float):
+    if name == "llama_decoder_step":
+        return ms_per_step * 1000.0, "us/step", False
+    if meta.get("flops", 0) == 0:
+        return meta["bytes"] / (ms_per_step * 1e-3) / 1e9, "GB/s", True
+    return meta["flops"] / (ms_per_step * 1e-3) / 1e12, "TFLOP/s", True
+
+
+def _roofline(w: dict, k_t: dict, compute_dtype: str) -> dict:
+    if w["part"] is not None:
+        part = next(p for p in k_t.get("parts", []) if p["name"] == w["part"])
+        mean_ms = part["mean_ms"]
+        kernel = w["part"]
+    else:
+        mean_ms = k_t["mean_ms"]
+        kernel = None
+    sec = mean_ms * 1e-3
+    if w["bound"] == "hbm":
+        achieved = w["per_launch"] / sec / 1e9
+        peak, unit = HBM_PEAK_GBPS, "GB/s"
+    else:
+        achieved = w["per_launch"] / sec / 1e12
+        peak, unit = MFMA_PEAK_TFLOPS[compute_dtype], "TFLOP/s"
+    out = {"bound": w["bound"], "achieved": achieved, "peak": peak, "unit": unit,
+           "frac": achieved / peak, "traffic": _traffic(kernel), "kernel_mean_us": mean_ms * 1e3}
+    if kernel:
+        out["kernel"] = kernel
+    return out
+
+
+def _traffic(kernel) -> float | None:
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (profiles/traffic.json), calibrated against a plain copy; None if
+    no counter run has been recorded for this kernel."""
+    p = REPO / "profiles" / "traffic.json"
+    if not p.is_file():
+        return None
+    try:
+        return json.loads(p.read_text()).get(kernel or "", {}).get("bytes_per_launch")
+    except Exception:
+        return None
+
+
+def _blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+        n = [i.get("num_threads", 0) for i in threadpool_info() if i.get("user_api") == "blas"]
+        return max(n) if n else 1
+    except Exception:
+        return os.cpu_count() or 1
+
+
+def _cpu_baseline(name: str, inputs, meta: dict) -> dict:
+    """Time the float64 oracle on a bounded sample of the workload."""
+    import numpy as np
+
+    import oracle
+
+    f = oracle.as_f64
+
+    def timed(fn, budget_s=10.0, max_iters=5):
+        fn()   # warm
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < max_iters and (time.perf_counter() - t_start) < budget_s:
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        times.sort()
+        return times[len(times) // 2], len(times)
+
+    if name == "llama_decoder_step":
+        args = [f(t) for t in inputs]
+        sec, n = timed(lambda: oracle.llama_decoder_step(*args, n_heads=_H, n_kv_heads=_HKV),
+                       budget_s=15.0, max_iters=3)
+        return {"value": sec * 1e6, "unit": "us/step", "cores": _blas_threads(), "kind": "port",
+                "sample": f"full decode step (B=16, L=2048) in float64 numpy, median of {n}"}
+    if name == "transpose_2d":
+        a = inputs[0].numpy()
+        sec, n = timed(lambda: oracle.transpose(a))
+        return {"value": meta["bytes"] / sec / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"full 8192x8192 fp32 transpose (numpy copy), median of {n}"}
+    if name == "sqr_mm":
+        a, b = f(inputs[0]), f(inputs[1])
+        sec, n = timed(lambda: oracle.matmul(a, b))
+        return {"value": meta["flops"] / sec / 1e12, "unit": "TFLOP/s", "cores": _blas_threads(),
+                "kind": "port", "sample": f"full 1024^3 GEMM in float64 numpy, median of {n}"}
+    if name == "conv2d":
+        x, w = f(inputs[0]), f(inputs[1])
+        sec, n = timed(lambda: oracle.conv2d_nhwc(x, w, 1, 1), max_iters=3)
+        return {"value": meta["flops"] / sec / 1e12, "unit": "TFLOP/s", "cores": _blas_threads(),
+                "kind": "port", "sample": f"full conv2d in float64 numpy, median of {n}"}
+    if name == "large_mm":
+        rows = 512
+        a = f(inputs[0][:rows])
+        b = f(inputs[1])
+        sec, n = timed(lambda: oracle.matmul(a, b), max_iters=3)
+        flops = 2.0 * rows * 8192 * 8192
+        return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": _blas_threads(),
+                "kind": "port",
+                "sample": f"{rows} of 8192 rows of the 8192^3 GEMM in float64 numpy, median of {n}"}
+    return None
+
+
+def _run_workload(name, steps, warmup, want_cpu):
+    import torch
+
+    from metalbench_amd import helpers as H
+    from metalbench_amd import native
+
+    b = H.load_baseline(name)
+    meta = b.meta
+    inputs = b.make_inputs(0)
+    dev = torch.device("cuda", 0)
+    d_in = [t.to(dev) for t in inputs]
+    d_out = [torch.zeros(tuple(o.shape), dtype=H.torch_dtype(o.dtype), device=dev)
+             for o in b.outputs]
+    bindings = []
+    for binding, t, dt in zip(b.input_bindings, d_in, b.input_dtypes):
+        bindings.append(native.make_binding(binding, native.ROLE_INPUT, dt, t.data_ptr(),
+                                            t.numel() * t.element_size()))
+    for o, t in zip(b.outputs, d_out):
+        bindings.append(native.make_binding(o.binding, native.ROLE_OUTPUT, o.dtype,
+                                            t.data_ptr(), t.numel() * t.element_size()))
+    for s in b.scalars():
+        bindings.append(native.make_binding(s.binding, native.ROLE_SCALAR, s.dtype,
+                                            value=s.value))
+    kid = native.kernel_find(b.metal_function)
+    torch.cuda.synchronize()
+    if warmup > 0:
+        native.run(kid, bindings, 0, warmup, native.RUN_PIPELINED)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    k_t = native.run(kid, bindings, 0, steps, native.RUN_PIPELINED | native.RUN_PARTS)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1000.0
+    ms_per_step = wall_ms / steps
+
+    w = _work(name, meta)
+    value, unit, hib = _value_unit(name, meta, ms_per_step)
+    rec = {"value": value, "unit": unit, "higher_is_better": hib, "ms_per_step": ms_per_step,
+           "gpu_median_ms": k_t["median_ms"], "gpu_mean_ms": k_t["mean_ms"],
+           "roofline": _roofline(w, k_t, b.compute_dtype), "dtype": b.compute_dtype}
+    if k_t.get("parts"):
+        rec["parts"] = [{"name": p["name"], "mean_us": p["mean_ms"] * 1e3,
+                         **({"hbm_frac": w["parts"][p["name"]] / (p["mean_ms"] * 1e-3) / 1e9
+                             / HBM_PEAK_GBPS} if "parts" in w and p["name"] in w["parts"] else {})}
+                        for p in k_t["parts"]]
+    del d_in, d_out
+    torch.cuda.synchronize()
+    if want_cpu:
+        rec["cpu_baseline"] = _cpu_baseline(name, inputs, meta)
+    return rec
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="llama_decoder_step")
+    ap.add_argument("--only", action="store_true", help="skip the other configurations")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (every config fits one MI355X; "
+              "the multi-GPU sharding is described in DESIGN.md, not run). Use --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from metalbench_amd import native
+    native.init(0)
+    names = native.kernel_names()
+
+    others = [n for n in ("transpose_2d", "sqr_mm", "conv2d", "large_mm") if n != args.workload]
+    if args.only:
+        others = []
+    rank0 = True
+    head = _run_workload(args.workload, args.steps, args.warmup, not args.no_cpu_baseline)
+    kernels = {}
+    for n in others:
+        from metalbench_amd import helpers as H
+        fn = H.load_baseline(n).metal_function
+        if fn not in names:
+            kernels[n] = {"status": "not built"}
+            continue
+        print(f"[bench] {n} ...", file=sys.stderr, flush=True)
+        kernels[n] = _run_workload(n, args.steps, args.warmup, not args.no_cpu_baseline)
+
+    from metalbench_amd import helpers as H
+    meta = H.load_baseline(args.workload).meta
+    if args.workload == "llama_decoder_step":
+        config = {"workload": args.workload, "batch": _B, "kv_len": _L, "d_model": _D,
+                  "n_heads": _H, "n_kv_heads": _HKV, "head_dim": _DH, "d_ff": _FF,
+                  "rope_theta": 500000.0, "parallelism": "single-gpu"}
+    else:
+        config = {"workload": args.workload, "input_shapes": meta["input_shapes"],
+                  "parallelism": "single-gpu"}
+    line = {
+        "metric": METRIC,
+        "value": head["value"],
+        "unit": head["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": head["higher_is_better"],
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": head["dtype"],
+        "data": "synthetic (seed 0; registry input_init distributions)",
+        "config": config,
+        "roofline": head["roofline"],
+        "cpu_baseline": head.get("cpu_baseline"),
+        "gpu_mean_ms": head["gpu_mean_ms"],
+        "parts": head.get("parts"),
+        "kernels": kernels,
+        "device": torch.cuda.get_device_name(0),
+    }
+    if rank0:
+        print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

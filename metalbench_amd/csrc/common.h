@@ -1,0 +1,87 @@
+// Internal declarations shared by the libmbhip.so translation units.
+// Nothing here is part of the C ABI (that is include/mbhip.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+
+#include "../../include/mbhip.h"
+
+namespace mb {
+
+// ---- errors ---------------------------------------------------------------
+// Records `msg` for mb_last_error() and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+#define MB_HIP_TRY(expr)                                                     \
+    do {                                                                     \
+        hipError_t _e = (expr);                                              \
+        if (_e != hipSuccess)                                                \
+            return ::mb::fail(MB_E_HIP, "%s failed: %s (%s:%d)", #expr,      \
+                              hipGetErrorString(_e), __FILE__, __LINE__);    \
+    } while (0)
+
+// Checks the launch that was just enqueued.
+#define MB_LAUNCH_CHECK(name)                                                \
+    do {                                                                     \
+        hipError_t _e = hipGetLastError();                                   \
+        if (_e != hipSuccess)                                                \
+            return ::mb::fail(MB_E_HIP, "launch of %s failed: %s", name,     \
+                              hipGetErrorString(_e));                        \
+    } while (0)
+
+// ---- library state ----------------------------------------------------------
+bool initialized();
+hipStream_t stream_or_default(void* s);   // NULL -> current library stream
+
+// Library-owned device workspace, grown on demand, freed by mb_shutdown().
+// Returns nullptr (and sets the error) on allocation failure.
+void* workspace(size_t bytes);
+
+// ---- per-kernel timing marks ---------------------------------------------------
+// A multi-kernel entry calls mark(i, name) right before enqueuing kernel i.
+// When timing parts, mb_run records an event there.
+struct PartMarks {
+    hipEvent_t* events = nullptr;   // n_max events, or nullptr
+    int n_max = 0;
+    int n = 0;
+    const char* names[MB_MAX_PARTS] = {};
+    void mark(hipStream_t s, const char* name) {
+        if (n < MB_MAX_PARTS) names[n] = name;
+        if (events && n < n_max) (void)hipEventRecord(events[n], s);
+        ++n;
+    }
+};
+
+// ---- bindings ---------------------------------------------------------------
+struct Bindings {
+    const mb_binding* slot[32] = {};
+    // Fetch binding `idx` and check role, dtype and (if min_bytes > 0) size.
+    int buffer(uint32_t idx, uint32_t dtype, uint64_t min_bytes, bool output,
+               void** ptr, const char* what) const;
+    int u32(uint32_t idx, uint32_t* v, const char* what) const;
+    int f32(uint32_t idx, float* v, const char* what) const;
+};
+
+// One registry entry: the `metal_function` name and its launcher.
+struct KernelEntry {
+    const char* name;
+    int (*launch)(const Bindings&, hipStream_t, PartMarks*);
+    const void* dominant_kernel;   // device function for hipFuncGetAttributes
+    int n_parts;
+};
+
+// Registration hooks, one per translation unit (called in a fixed order).
+void register_kernel(const KernelEntry& e);
+void register_transpose();
+void register_copy();
+void register_gemm_f32();
+void register_conv2d();
+void register_gemm_bf16();
+void register_decoder();
+
+static inline uint32_t cdiv(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
+
+}  // namespace mb

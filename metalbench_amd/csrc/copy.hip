@@ -1,0 +1,84 @@
+// Plain fp32 copy dst = src.
+//
+// No reference counterpart.  It is the calibration kernel for two things:
+//  * the HBM ceiling actually reachable on the box (a read + write stream of
+//    known size, the same traffic pattern as a transpose);
+//  * the scale factor of the FETCH_SIZE / WRITE_SIZE counters: a copy of N
+//    bytes must read N and write N bytes of HBM, so counter / N calibrates
+//    counter readings taken on the other kernels.
+#include "common.h"
+
+namespace mb {
+namespace {
+
+constexpr int THREADS = 256;
+constexpr int VEC_PER_THREAD = 4;   // four float4 in flight per lane
+
+__global__ __launch_bounds__(THREADS)
+void copy_f32_kernel(const float4* __restrict__ src, float4* __restrict__ dst, uint64_t n4) {
+    const uint64_t base = ((uint64_t)blockIdx.x * THREADS * VEC_PER_THREAD) + threadIdx.x;
+    float4 v[VEC_PER_THREAD];
+#pragma unroll
+    for (int i = 0; i < VEC_PER_THREAD; ++i) {
+        const uint64_t j = base + (uint64_t)i * THREADS;
+        if (j < n4) v[i] = src[j];
+    }
+#pragma unroll
+    for (int i = 0; i < VEC_PER_THREAD; ++i) {
+        const uint64_t j = base + (uint64_t)i * THREADS;
+        if (j < n4) dst[j] = v[i];
+    }
+}
+
+__global__ void copy_f32_tail_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                                     uint64_t start, uint64_t n) {
+    const uint64_t i = start + threadIdx.x;
+    if (i < n) dst[i] = src[i];
+}
+
+int launch_copy(const float* src, float* dst, uint64_t n, hipStream_t s) {
+    if (n == 0) return MB_OK;
+    if (!src || !dst) return fail(MB_E_ARG, "copy_f32: null pointer");
+    if (((uintptr_t)src | (uintptr_t)dst) & 15)
+        return fail(MB_E_ARG, "copy_f32: pointers must be 16-byte aligned");
+    const uint64_t n4 = n / 4;
+    if (n4) {
+        const uint64_t per_block = (uint64_t)THREADS * VEC_PER_THREAD;
+        const uint64_t blocks = (n4 + per_block - 1) / per_block;
+        if (blocks > 0x7fffffffull) return fail(MB_E_ARG, "copy_f32: size too large");
+        hipLaunchKernelGGL(copy_f32_kernel, dim3((uint32_t)blocks), dim3(THREADS), 0, s,
+                           reinterpret_cast<const float4*>(src), reinterpret_cast<float4*>(dst), n4);
+        MB_LAUNCH_CHECK("copy_f32");
+    }
+    if (n4 * 4 < n) {
+        hipLaunchKernelGGL(copy_f32_tail_kernel, dim3(1), dim3(64), 0, s, src, dst, n4 * 4, n);
+        MB_LAUNCH_CHECK("copy_f32_tail");
+    }
+    return MB_OK;
+}
+
+// Registry launcher: src@0 (input f32), dst@1 (output f32), n@2 (elements).
+int run_copy(const Bindings& bs, hipStream_t s, PartMarks*) {
+    uint32_t n;
+    int rc;
+    if ((rc = bs.u32(2, &n, "n"))) return rc;
+    void *a, *b;
+    if ((rc = bs.buffer(0, MB_DTYPE_F32, (uint64_t)n * 4, false, &a, "src")) ||
+        (rc = bs.buffer(1, MB_DTYPE_F32, (uint64_t)n * 4, true, &b, "dst")))
+        return rc;
+    return launch_copy((const float*)a, (float*)b, n, s);
+}
+
+}  // namespace
+
+void register_copy() {
+    register_kernel({"copy_f32", run_copy, reinterpret_cast<const void*>(&copy_f32_kernel), 1});
+}
+
+}  // namespace mb
+
+extern "C" int mb_launch_copy_f32(const float* src, float* dst, uint64_t n, void* stream) {
+    mb::clear_error();
+    if (!mb::initialized()) return mb::fail(MB_E_STATE, "mb_init() has not been called");
+    return mb::launch_copy(src, dst, n, mb::stream_or_default(stream));
+}

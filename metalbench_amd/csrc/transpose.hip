@@ -1,0 +1,118 @@
+// 2D fp32 transpose B[c][r] = A[r][c], bit exact.
+//
+// Spec: reference mlx/kernels/common/transpose_2d.py:10-11 (mx.transpose),
+// registry mlx/kernels/common/registry.py:165-179 (input binding 0, output
+// binding 1, scalars rows@2 and cols@3, rtol = atol = 0).
+//
+// gfx950 design (HBM bound, 0 flops, 2*rows*cols*4 algorithmic bytes):
+//  * one 256-thread workgroup (4 waves of 64) moves one 64x64 tile;
+//  * global reads: each lane loads four 16-byte float4 along a row of A, so a
+//    wave reads four contiguous 256-byte row segments per instruction;
+//  * the tile goes through LDS as float[64][65]: the +1 column of padding
+//    makes both the row-wise writes and the column-wise reads hit 64 distinct
+//    4-byte banks per wave (bank = (row + col) mod 64);
+//  * global writes: each lane stores four float4 along a row of B.
+//  * Tiles whose rows or cols run past the edge take a guarded scalar path, so
+//    any shape (including empty and ragged ones) is handled.
+#include "common.h"
+
+namespace mb {
+namespace {
+
+constexpr int TILE = 64;
+constexpr int THREADS = 256;
+
+__global__ __launch_bounds__(THREADS)
+void transpose_2d_f32_kernel(const float* __restrict__ a, float* __restrict__ b,
+                             uint32_t rows, uint32_t cols, uint32_t tiles_c) {
+    __shared__ float tile[TILE][TILE + 1];
+
+    const uint32_t tr = blockIdx.x / tiles_c;
+    const uint32_t tc = blockIdx.x - tr * tiles_c;
+    const uint32_t r0 = tr * TILE;
+    const uint32_t c0 = tc * TILE;
+    const uint32_t tx = threadIdx.x & 15;   // float4 column within the tile
+    const uint32_t ty = threadIdx.x >> 4;   // 0..15
+
+    const bool full = (r0 + TILE <= rows) && (c0 + TILE <= cols) &&
+                      ((cols & 3) == 0) && ((rows & 3) == 0);
+    if (full) {
+        float4 v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            v[i] = *reinterpret_cast<const float4*>(
+                a + (size_t)(r0 + ty + 16 * i) * cols + c0 + 4 * tx);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            tile[ty + 16 * i][4 * tx + 0] = v[i].x;
+            tile[ty + 16 * i][4 * tx + 1] = v[i].y;
+            tile[ty + 16 * i][4 * tx + 2] = v[i].z;
+            tile[ty + 16 * i][4 * tx + 3] = v[i].w;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t j = ty + 16 * i;          // row of B inside the tile
+            float4 o;
+            o.x = tile[4 * tx + 0][j];
+            o.y = tile[4 * tx + 1][j];
+            o.z = tile[4 * tx + 2][j];
+            o.w = tile[4 * tx + 3][j];
+            *reinterpret_cast<float4*>(b + (size_t)(c0 + j) * rows + r0 + 4 * tx) = o;
+        }
+    } else {
+        // Edge tile: one element per lane per step, guarded.
+        const uint32_t lx = threadIdx.x & 63;
+        const uint32_t ly = threadIdx.x >> 6;   // 0..3
+        for (uint32_t i = ly; i < TILE; i += 4) {
+            const uint32_t r = r0 + i, c = c0 + lx;
+            if (r < rows && c < cols) tile[i][lx] = a[(size_t)r * cols + c];
+        }
+        __syncthreads();
+        for (uint32_t j = ly; j < TILE; j += 4) {
+            const uint32_t c = c0 + j, r = r0 + lx;   // B[c][r] = A[r][c]
+            if (c < cols && r < rows) b[(size_t)c * rows + r] = tile[lx][j];
+        }
+    }
+}
+
+int launch_transpose(const float* a, float* b, uint32_t rows, uint32_t cols, hipStream_t s) {
+    if (rows == 0 || cols == 0) return MB_OK;
+    if (!a || !b) return fail(MB_E_ARG, "transpose_2d_f32: null pointer");
+    const uint32_t tiles_r = cdiv(rows, TILE), tiles_c = cdiv(cols, TILE);
+    const uint64_t nblocks = (uint64_t)tiles_r * tiles_c;
+    if (nblocks > 0x7fffffffull) return fail(MB_E_ARG, "transpose_2d_f32: shape too large");
+    hipLaunchKernelGGL(transpose_2d_f32_kernel, dim3((uint32_t)nblocks), dim3(THREADS), 0, s,
+                       a, b, rows, cols, tiles_c);
+    MB_LAUNCH_CHECK("transpose_2d_f32");
+    return MB_OK;
+}
+
+// Registry launcher: A@0 (input f32), B@1 (output f32), rows@2, cols@3.
+int run_transpose(const Bindings& bs, hipStream_t s, PartMarks*) {
+    uint32_t rows, cols;
+    int rc;
+    if ((rc = bs.u32(2, &rows, "rows")) || (rc = bs.u32(3, &cols, "cols"))) return rc;
+    const uint64_t nbytes = (uint64_t)rows * cols * 4;
+    void *a, *b;
+    if ((rc = bs.buffer(0, MB_DTYPE_F32, nbytes, false, &a, "A")) ||
+        (rc = bs.buffer(1, MB_DTYPE_F32, nbytes, true, &b, "B")))
+        return rc;
+    return launch_transpose((const float*)a, (float*)b, rows, cols, s);
+}
+
+}  // namespace
+
+void register_transpose() {
+    register_kernel({"transpose_2d_f32", run_transpose,
+                     reinterpret_cast<const void*>(&transpose_2d_f32_kernel), 1});
+}
+
+}  // namespace mb
+
+extern "C" int mb_launch_transpose_2d_f32(const float* a, float* b, uint32_t rows,
+                                          uint32_t cols, void* stream) {
+    mb::clear_error();
+    if (!mb::initialized()) return mb::fail(MB_E_STATE, "mb_init() has not been called");
+    return mb::launch_transpose(a, b, rows, cols, mb::stream_or_default(stream));
+}

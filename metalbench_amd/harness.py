@@ -1,0 +1,456 @@
+"""MetalBench harness on gfx950: dispatch a kernel, time it, grade it.
+
+    python mlx/scripts/harness.py <name> [--target speed|compute|memory|stable|balanced]
+                                         [--iters 200] [--warmup 10] [--seed 0]
+                                         [--save] [--no-session] [--dry-run]
+                                         [--mlx-only | --metal-only] [--cpu-iters N]
+
+Same flow, report text, exit codes and persistence as reference
+mlx/scripts/harness.py:52-508, with the gfx950 backend in place of Metal:
+  * the kernel runs in-process through libmbhip.so (`mb_run`), on device
+    buffers that torch allocates; no manifest/.bin files (reference :36-49, :74-98);
+  * the `mlx ref` line times the registry's Model spec on the host CPU
+    (MLX does not run on this platform); the correctness gate compares against
+    the same spec's output, in float64, with the reference's rule
+    |a - b| <= atol + rtol*|b| (reference :26-33);
+  * the `roofline` line prices the kernel against MI355X peaks for the dtype
+    it computes in.
+`--metal-only` / `--mlx-only` keep their reference meaning: the GPU kernel only
+(no spec timing, no correctness gate) / the CPU spec only.
+"""
+from __future__ import annotations
+
+import argparse
+import datetime as _dt
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+
+if __package__ in (None, ""):
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
+    from metalbench_amd import helpers as H          # noqa: E402
+    from metalbench_amd import native, roofline      # noqa: E402
+    from metalbench_amd.timing import time_cpu       # noqa: E402
+else:
+    from . import helpers as H
+    from . import native, roofline
+    from .timing import time_cpu
+
+
+def _to_np64(x) -> np.ndarray:
+    if hasattr(x, "detach"):
+        x = x.detach().float().cpu().numpy()
+    return np.asarray(x).astype(np.float64)
+
+
+def _allclose(actual, expected, rtol, atol):
+    """float64 |a - b| <= atol + rtol*|b| (reference harness.py:26-33)."""
+    a = _to_np64(actual)
+    b = _to_np64(expected)
+    if a.shape != b.shape:
+        return False, float("inf")
+    if a.size == 0:
+        return True, 0.0
+    diff = np.abs(a - b)
+    tol = atol + rtol * np.abs(b)
+    ok = bool(np.all(diff <= tol))     # NaN anywhere fails
+    return ok, float(np.nanmax(diff)) if not np.isnan(diff).all() else float("inf")
+
+
+def _run_native(b, inputs, warmup, iters, flags=native.RUN_SYNC_EACH):
+    """Upload inputs, bind, time through mb_run, download outputs.  Replaces
+    the host subprocess (reference harness.py:36-49 and main.mm:125-171)."""
+    import torch
+    native.init(0)
+    dev = torch.device("cuda", 0)
+    d_in = [t.to(dev) for t in inputs]
+    d_out = [torch.zeros(tuple(o.shape), dtype=H.torch_dtype(o.dtype), device=dev)
+             for o in b.outputs]
+    torch.cuda.synchronize()
+    bindings = []
+    for binding, t, dt in zip(b.input_bindings, d_in, b.input_dtypes):
+        bindings.append(native.make_binding(binding, native.ROLE_INPUT, dt, t.data_ptr(),
+                                            t.numel() * t.element_size()))
+    for o, t in zip(b.outputs, d_out):
+        bindings.append(native.make_binding(o.binding, native.ROLE_OUTPUT, o.dtype,
+                                            t.data_ptr(), t.numel() * t.element_size()))
+    for s in b.scalars():
+        bindings.append(native.make_binding(s.binding, native.ROLE_SCALAR, s.dtype,
+                                            value=s.value))
+    kid = native.kernel_find(b.metal_function)
+    k_t = native.run(kid, bindings, warmup, iters, flags)
+    outs = [t.cpu() for t in d_out]
+    attrs = native.kernel_attrs(kid)
+    k_t["tg_static_mem_bytes"] = attrs["static_lds_bytes"]
+    k_t["pso_max_threads_per_tg"] = attrs["max_threads_per_block"]
+    k_t["vgprs"] = attrs["num_regs"]
+    k_t["hip_device"] = H.chip_info()["name"]
+    del d_in, d_out
+    return k_t, outs
+
+
+def _cpu_iters(b, iters, override):
+    if override:
+        return int(override)
+    return max(1, min(int(iters), int(b.meta.get("cpu_iters", iters))))
+
+
+def evaluate(name, *, seed, warmup, iters, dry_run=False, profile=False, solo=None,
+             cpu_iters=None):
+    b = H.load_baseline(name)
+    inputs = b.make_inputs(seed)
+    chip = H.chip_info()
+    c_iters = _cpu_iters(b, iters, cpu_iters)
+
+    if solo == "mlx":
+        ref_out = b.reference(*inputs)
+        r_t = time_cpu(b.reference, *inputs, warmup=1, iters=c_iters)
+        return {"task": name, "chip": chip, "solo": "mlx",
+                "reference_timing": r_t, "correct": True,
+                "metrics": {"stability": max(0.0,
+                            1.0 - abs(r_t["median_ms"] - r_t["mean_ms"]) / r_t["mean_ms"]
+                            if r_t["mean_ms"] > 0 else 0.0)},
+                "outputs": []}
+
+    manifest = H.build_manifest(b, inputs, warmup=warmup, iters=iters,
+                                chip_type=chip["type"], profile=profile)
+    if dry_run:
+        return {"task": name, "dry_run": True, "manifest": manifest}
+
+    k_t, kernel_outs = _run_native(b, inputs, warmup, iters)
+
+    def _kernel_metrics(m):
+        median_s = k_t["median_ms"] / 1000.0
+        if median_s > 0:
+            if (f := b.flops(inputs)) is not None:
+                m["gflops"] = f / median_s / 1e9
+            if (nb := b.bytes(inputs)) is not None:
+                m["gbps"] = nb / median_s / 1e9
+            if f is not None and nb is not None and nb > 0:
+                m["arith_intensity"] = f / nb
+        mean_ms = k_t["mean_ms"]
+        cv = abs(k_t["median_ms"] - mean_ms) / mean_ms if mean_ms > 0 else 0.0
+        m["stability"] = max(0.0, 1.0 - cv)
+        return m
+
+    if solo == "metal":
+        return {"task": name, "chip": chip, "solo": "metal", "correct": True,
+                "metrics": _kernel_metrics({}), "kernel_timing": k_t, "outputs": [],
+                "compute_dtype": b.compute_dtype}
+
+    ref_out = b.reference(*inputs)
+    ref_outs = list(ref_out) if isinstance(ref_out, (list, tuple)) else [ref_out]
+    r_t = time_cpu(b.reference, *inputs, warmup=1 if c_iters > 1 else 0, iters=c_iters)
+    r_t["label"] = "cpu spec (torch, %d threads)" % r_t.get("threads", 0)
+
+    if len(kernel_outs) != len(ref_outs):
+        raise RuntimeError(f"{name}: kernel={len(kernel_outs)} outputs, ref={len(ref_outs)}")
+
+    per_output = []
+    for k, r in zip(kernel_outs, ref_outs):
+        ok, max_err = _allclose(k, r, b.rtol, b.atol)
+        per_output.append({"ok": ok, "max_err": max_err})
+
+    correct = all(o["ok"] for o in per_output)
+    speedup = (r_t["median_ms"] / k_t["median_ms"]) if k_t["median_ms"] > 0 else float("inf")
+    metrics = _kernel_metrics({"speedup": speedup})
+
+    return {
+        "task": name,
+        "chip": chip,
+        "metal_device": k_t.get("hip_device", "unknown"),
+        "tg_static_mem_bytes": k_t.get("tg_static_mem_bytes"),
+        "pso_max_threads_per_tg": k_t.get("pso_max_threads_per_tg"),
+        "correct": correct,
+        "metrics": metrics,
+        "speedup": speedup,
+        "kernel_timing": k_t,
+        "reference_timing": r_t,
+        "outputs": per_output,
+        "compute_dtype": b.compute_dtype,
+    }
+
+
+# Each target picks ONE primary metric to optimize (reference harness.py:176-186).
+TARGETS = {
+    "speed": lambda m: m.get("speedup", 0.0),
+    "compute": lambda m: m.get("gflops", 0.0),
+    "memory": lambda m: m.get("gbps", 0.0),
+    "stable": lambda m: m.get("stability", 0.0),
+    "balanced": lambda m: (
+        0.5 * m.get("speedup", 0.0)
+        + 0.3 * (m.get("gflops", 0.0) / 1000.0)
+        + 0.2 * m.get("stability", 0.0)
+    ),
+}
+
+
+def grade(metrics, target):
+    fn = TARGETS.get(target)
+    if fn is None:
+        raise SystemExit(f"unknown target '{target}'; pick {list(TARGETS)}")
+    return float(fn(metrics))
+
+
+def update_session(name, result, target, iters, session_path=None):
+    """Best run per (chip bucket, kernel) in session.json, same keys as
+    reference harness.py:196-247: updated only if correct and faster.  The
+    kernel source stored is the HIP file that implements the kernel."""
+    if not result.get("correct"):
+        return False, "skipped (incorrect)"
+    session_path = Path(session_path) if session_path else H.SESSION_PATH
+    bucket = result["chip"]["bucket"]
+    new_ms = result["kernel_timing"]["median_ms"]
+
+    src_path = H.find_kernel_source(name)
+    src_text = src_path.read_text() if src_path else None
+
+    session = {}
+    if session_path.exists():
+        try:
+            session = json.loads(session_path.read_text())
+        except Exception:
+            session = {}
+
+    chip_section = session.setdefault(bucket, {})
+    prev = chip_section.get(name)
+    prev_ms = prev["best_time_ms"] if prev else None
+    if prev_ms is not None and new_ms >= prev_ms:
+        return False, f"current best {prev_ms:.3f} ms holds (this run {new_ms:.3f} ms)"
+
+    try:
+        rel_src = str(src_path.relative_to(H.REPO_ROOT)) if src_path else None
+    except ValueError:
+        rel_src = str(src_path)
+    chip_section[name] = {
+        "best_time_ms": new_ms,
+        "speedup_vs_mlx": result["metrics"]["speedup"],
+        "gflops": result["metrics"].get("gflops"),
+        "gbps": result["metrics"].get("gbps"),
+        "arith_intensity": result["metrics"].get("arith_intensity"),
+        "stability": result["metrics"]["stability"],
+        "tg_static_mem_bytes": result.get("tg_static_mem_bytes"),
+        "pso_max_threads_per_tg": result.get("pso_max_threads_per_tg"),
+        "iters": iters,
+        "target": target,
+        "max_err": max((o["max_err"] for o in result["outputs"]), default=0.0),
+        "metal_source_path": rel_src,
+        "metal_source": src_text,
+        "updated_at": _dt.datetime.now(_dt.timezone.utc).isoformat(timespec="seconds"),
+    }
+    session_path.write_text(json.dumps(session, indent=2) + "\n")
+    delta = "" if prev_ms is None else f" (was {prev_ms:.3f} ms, Δ {prev_ms - new_ms:+.3f})"
+    return True, f"new best {new_ms:.3f} ms{delta}"
+
+
+def _bytes_human(n):
+    for u in ("B", "KB", "MB", "GB"):
+        if n < 1024:
+            return f"{n:.0f}{u}"
+        n /= 1024
+    return f"{n:.0f}TB"
+
+
+def _roofline_line(result, m, k_t):
+    f = m.get("gflops", 0) * (k_t["median_ms"] / 1000.0) * 1e9 if "gflops" in m else 0
+    nb = m.get("gbps", 0) * (k_t["median_ms"] / 1000.0) * 1e9 if "gbps" in m else 0
+    rl = roofline.classify(result["chip"]["type"], f, nb, k_t["median_ms"],
+                           result.get("compute_dtype", "f32"))
+    return roofline.format_line(rl)
+
+
+def _print_report(result, target, score):
+    """Human-readable report, same labels as reference harness.py:257-333."""
+    chip = result["chip"]
+    m = result["metrics"]
+    k_t = result.get("kernel_timing")
+    r_t = result.get("reference_timing")
+    outs = result.get("outputs", [])
+    solo = result.get("solo")
+
+    line = "─" * 72
+    if solo:
+        side = "MLX only" if solo == "mlx" else "Metal only"
+        print(line); print(f"  {result['task']}    [{side}]"); print(line)
+        print(f"  device      : {chip['name']} ({chip['type']})  "
+              f"{chip['cpu_cores']} CPU / {chip['gpu_cores']} GPU / "
+              f"{chip['ram_bytes']/1e9:.0f} GB")
+        t = k_t if solo == "metal" else r_t
+        label = "metal kernel" if solo == "metal" else "mlx ref"
+        print(f"  {label:11s} : {t['median_ms']:.3f} ms  "
+              f"(min {t['min_ms']:.3f}, mean {t['mean_ms']:.3f}, n={t['iters']})")
+        if "gflops" in m: print(f"  compute     : {m['gflops']:.1f} GFLOPS")
+        if "gbps" in m: print(f"  bandwidth   : {m['gbps']:.1f} GB/s")
+        if "stability" in m:
+            print(f"  stability   : {m['stability']:.2f}")
+        if solo == "metal":
+            print(_roofline_line(result, m, k_t))
+        print(line)
+        return
+
+    print(line)
+    print(f"  {result['task']}    target={target}   score={score:.3f}")
+    print(line)
+    print(f"  device      : {chip['name']} ({chip['type']})  "
+          f"{chip['cpu_cores']} CPU / {chip['gpu_cores']} GPU / "
+          f"{chip['ram_bytes']/1e9:.0f} GB")
+    if result.get("tg_static_mem_bytes") is not None:
+        print(f"  occupancy   : tg_mem={_bytes_human(result['tg_static_mem_bytes'])}  "
+              f"max_thr/tg={result['pso_max_threads_per_tg']}")
+    print()
+    status = "✓ correct " if result["correct"] else "✗ INCORRECT"
+    max_err = max((o["max_err"] for o in outs), default=0.0)
+    print(f"  correctness : {status}    max_err={max_err:.3e}")
+    print(f"  speedup     : {m.get('speedup', 0):.2f}× vs MLX")
+    print(f"  kernel      : {k_t['median_ms']:.3f} ms  "
+          f"(min {k_t['min_ms']:.3f}, mean {k_t['mean_ms']:.3f}, n={k_t['iters']})")
+    print(f"  mlx ref     : {r_t['median_ms']:.3f} ms  "
+          f"(min {r_t['min_ms']:.3f}, mean {r_t['mean_ms']:.3f}, n={r_t['iters']})"
+          f"  [{r_t.get('label', 'cpu spec')}]")
+    if "gflops" in m:
+        print(f"  compute     : {m['gflops']:.1f} GFLOPS")
+    if "gbps" in m:
+        print(f"  bandwidth   : {m['gbps']:.1f} GB/s")
+    if "arith_intensity" in m:
+        print(f"  arith int.  : {m['arith_intensity']:.1f} FLOPs/byte")
+    print(f"  stability   : {m['stability']:.2f}  (1.0 = perfectly consistent)")
+    try:
+        print(_roofline_line(result, m, k_t))
+    except Exception:
+        pass
+    for p in k_t.get("parts", []):
+        print(f"    part {p['name']:24s} {p['median_ms']*1000:8.1f} µs")
+    print()
+    print(f"  {'target':>10s}   {'score':>10s}")
+    print(f"  {'-'*10}   {'-'*10}")
+    for t in ("speed", "compute", "memory", "stable", "balanced"):
+        s = grade(m, t)
+        print(f"  {t:>10s}   {s:10.3f}")
+    print(line)
+
+
+def _update_best_times_md(session_path=None, out_path=None):
+    """Regenerate best_times.md from session.json (reference harness.py:336-384)."""
+    sp = Path(session_path) if session_path else H.SESSION_PATH
+    if not sp.exists():
+        return
+    session = json.loads(sp.read_text())
+
+    def _type(name):
+        if "mm" in name or "matmul" in name:
+            return "matmul"
+        if "transpose" in name:
+            return "copy"
+        if "conv" in name:
+            return "conv"
+        if "decoder" in name:
+            return "model"
+        return "?"
+
+    chip_order = sorted(session.keys())
+    chip_header = " | ".join(f"{c} HIP | {c} speedup" for c in chip_order)
+    lines = ["# MetalBench Best Times (gfx950 backend)", "",
+             f"| kernel | type | {chip_header} |",
+             "|---|" + "|---|" * (len(chip_order) * 2 + 1)]
+    all_names = set()
+    for cdata in session.values():
+        all_names.update(cdata.keys())
+    for name in sorted(all_names):
+        cols = [name, _type(name)]
+        for chip in chip_order:
+            d = session[chip].get(name, {})
+            ms, spd = d.get("best_time_ms"), d.get("speedup_vs_mlx")
+            cols.append(f"{ms:.3f}ms" if ms else "--")
+            cols.append(f"{spd:.1f}×" if spd else "--")
+        lines.append("| " + " | ".join(cols) + " |")
+    lines += ["", "---", f"**Chips:** {', '.join(chip_order)}", "",
+              "Speedup is against the CPU spec on the host cores (MLX is not available)."]
+    (Path(out_path) if out_path else H.REPO_ROOT / "best_times.md").write_text(
+        "\n".join(lines) + "\n")
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(prog="metalbench-harness")
+    ap.add_argument("name", nargs="?")
+    ap.add_argument("--_update_md", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--iters", type=int, default=200)
+    ap.add_argument("--cpu-iters", type=int, default=None,
+                    help="iterations of the CPU spec timing (default: registry cpu_iters)")
+    ap.add_argument("--dry-run", action="store_true")
+    ap.add_argument("--profile", action="store_true",
+                    help="record the request; counters come from rocprofv3 around this run")
+    ap.add_argument("--save", action="store_true",
+                    help="save full result JSON to results/<chip>/<name>.json")
+    ap.add_argument("--no-session", action="store_true", help="don't update session.json")
+    ap.add_argument("--target", default="speed", choices=list(TARGETS.keys()))
+    solo = ap.add_mutually_exclusive_group()
+    solo.add_argument("--mlx-only", action="store_true",
+                      help="time only the CPU spec (no GPU call)")
+    solo.add_argument("--metal-only", action="store_true",
+                      help="time only the gfx950 kernel (skip spec timing + correctness)")
+    args = ap.parse_args(argv)
+    solo_mode = "mlx" if args.mlx_only else ("metal" if args.metal_only else None)
+
+    if args._update_md:
+        _update_best_times_md()
+        return 0
+    if not args.name:
+        ap.error("kernel name required (or use --all from bench script)")
+
+    chip = H.chip_info()
+    if solo_mode != "mlx" and not args.dry_run and chip["type"] != "gfx950":
+        sys.exit(f"[error] this backend requires an AMD gfx950 (MI355X) GPU. "
+                 f"Detected: {chip.get('error', chip['name'])!r}.")
+
+    print(f"[chip] {chip['type']:>8s}  '{chip['name']}'  "
+          f"cpu={chip['cpu_cores']}  gpu={chip['gpu_cores']}  "
+          f"ram={chip['ram_bytes']/1e9:.0f}GB", file=sys.stderr)
+
+    try:
+        bf = H.load_baseline(args.name).best_for
+        if bf and "all" not in bf and chip["type"] not in bf:
+            print(f"[bench] kernel `{args.name}` BEST_FOR={list(bf)}; "
+                  f"current chip '{chip['type']}' not in that list", file=sys.stderr)
+        elif bf:
+            print(f"[bench] kernel `{args.name}` BEST_FOR={list(bf)}", file=sys.stderr)
+    except Exception:
+        pass
+
+    result = evaluate(args.name, seed=args.seed, warmup=args.warmup, iters=args.iters,
+                      dry_run=args.dry_run, profile=args.profile, solo=solo_mode,
+                      cpu_iters=args.cpu_iters)
+
+    if args.dry_run:
+        print(json.dumps(result["manifest"], indent=2))
+        return 0
+
+    score = grade(result["metrics"], args.target)
+    result["target"] = args.target
+    result["score"] = score
+    _print_report(result, args.target, score)
+
+    if solo_mode:
+        return 0
+
+    if args.save:
+        out_dir = H.RESULTS_ROOT / result["chip"]["bucket"]
+        out_dir.mkdir(parents=True, exist_ok=True)
+        out_path = out_dir / f"{args.name}.json"
+        out_path.write_text(json.dumps(result, indent=2, default=str))
+        print(f"saved → {out_path.relative_to(H.REPO_ROOT)}", file=sys.stderr)
+
+    if not args.no_session:
+        updated, why = update_session(args.name, result, args.target, args.iters)
+        rel = H.SESSION_PATH.relative_to(H.REPO_ROOT)
+        prefix = f"updated {rel}" if updated else f"{rel} unchanged"
+        print(f"{prefix} [{result['chip']['bucket']}/{args.name}]: {why}", file=sys.stderr)
+
+    return 0 if result["correct"] else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

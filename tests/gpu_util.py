@@ -1,0 +1,58 @@
+"""Helpers for the GPU parity tests: seeded inputs, launches through the C ABI."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from metalbench_amd import helpers as H
+from metalbench_amd import native
+
+
+def seeded(seed: int, shape, init=("normal", 0.0, 1.0), dtype="f32"):
+    gen = torch.Generator().manual_seed(seed)
+    return H.generate_input(gen, shape, init, dtype)
+
+
+def sync():
+    torch.cuda.synchronize()
+
+
+def launch(fn_name: str, *args):
+    """Call an mb_launch_* entry point on the library stream and wait."""
+    lib = native.load()
+    rc = getattr(lib, fn_name)(*args)
+    native.check(fn_name, rc)
+    sync()
+
+
+def ptr(t) -> int:
+    return t.data_ptr()
+
+
+def bits32(t) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int32).numpy()
+
+
+def run_registry(name: str, seed: int = 0, warmup: int = 1, iters: int = 2, inputs=None):
+    """Run a registry entry through mb_run (the harness path); returns
+    (baseline, inputs, outputs, timing)."""
+    from metalbench_amd import harness
+    b = H.load_baseline(name)
+    if inputs is None:
+        inputs = b.make_inputs(seed)
+    k_t, outs = harness._run_native(b, inputs, warmup, iters)
+    return b, inputs, outs, k_t
+
+
+def assert_close(actual, expected, rtol, atol, what=""):
+    a = np.asarray(actual, np.float64)
+    e = np.asarray(expected, np.float64)
+    assert a.shape == e.shape, (what, a.shape, e.shape)
+    diff = np.abs(a - e)
+    tol = atol + rtol * np.abs(e)
+    bad = ~(diff <= tol)
+    if bad.any():
+        idx = np.unravel_index(np.argmax(np.where(bad, diff - tol, -np.inf)), a.shape)
+        raise AssertionError(f"{what}: {int(bad.sum())} / {a.size} elements out of tolerance "
+                             f"(rtol={rtol}, atol={atol}); worst at {idx}: got {a[idx]!r}, "
+                             f"expected {e[idx]!r}, max |diff| {diff.max():.3e}")

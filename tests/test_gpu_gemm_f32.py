@@ -1,0 +1,50 @@
+"""fp32 MFMA GEMM (sqr_mm / rect_mm) on the GPU vs the float64 oracle.
+
+Tolerance: rtol = atol = 1e-4 for the sqr_mm config (BASELINE), scaled with
+sqrt(K) for the normal(0,1) shapes where |C| grows with K."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import assert_close, launch, ptr, run_registry, seeded
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("m,n,k", [
+    (1, 1, 1), (1, 64, 64), (64, 1, 64), (64, 64, 1), (64, 64, 64), (65, 33, 17),
+    (128, 256, 64), (100, 300, 96), (257, 129, 200), (512, 512, 512), (31, 1000, 36),
+])
+def test_matmul_f32_shapes(mb, dev, m, n, k):
+    a = seeded(m * 1000 + k, (m, k), ("uniform", -1.0, 1.0))
+    b = seeded(n * 1000 + k + 1, (k, n), ("uniform", -1.0, 1.0))
+    d_a, d_b = a.to(dev), b.to(dev)
+    d_c = torch.full((m, n), float("nan"), device=dev)
+    launch("mb_launch_matmul_f32", ptr(d_a), ptr(d_b), ptr(d_c), m, n, k, None)
+    want = oracle.matmul(a.numpy(), b.numpy())
+    assert_close(d_c.cpu().numpy(), want, 1e-4, 1e-4, f"matmul_f32 {m}x{n}x{k}")
+
+
+def test_matmul_f32_k0_gives_zeros(mb, dev):
+    d_c = torch.full((8, 8), 5.0, device=dev)
+    d_a = torch.zeros(1, device=dev)
+    launch("mb_launch_matmul_f32", ptr(d_a), ptr(d_a), ptr(d_c), 8, 8, 0, None)
+    assert torch.all(d_c.cpu() == 0.0)
+
+
+def test_matmul_f32_identity_exact(mb, dev):
+    a = seeded(3, (192, 192))
+    eye = torch.eye(192)
+    d_a, d_eye = a.to(dev), eye.to(dev)     # keep both alive across the launch
+    d_c = torch.zeros((192, 192), device=dev)
+    launch("mb_launch_matmul_f32", ptr(d_a), ptr(d_eye), ptr(d_c), 192, 192, 192, None)
+    assert torch.equal(d_c.cpu(), a)
+
+
+@pytest.mark.parametrize("name", ["sqr_mm", "rect_mm"])
+def test_matmul_registry_config(mb, name):
+    b, inputs, outs, _ = run_registry(name, seed=0)
+    want = oracle.matmul(inputs[0].numpy(), inputs[1].numpy())
+    tol = 1e-4 if name == "sqr_mm" else 1e-3
+    assert_close(outs[0].numpy(), want, tol, tol, name)

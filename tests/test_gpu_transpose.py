@@ -1,0 +1,48 @@
+"""transpose_2d_f32 on the GPU vs the oracle: bit exact (reference registry
+rtol = atol = 0, mlx/kernels/common/registry.py:165-179)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import bits32, launch, ptr, run_registry, seeded
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("rows,cols", [
+    (1, 1), (1, 7), (7, 1), (64, 64), (63, 65), (65, 63), (128, 192), (1000, 3),
+    (3, 1000), (333, 777), (1024, 2048), (2048, 1024), (4096, 64),
+])
+def test_transpose_bit_exact(mb, dev, rows, cols):
+    a = seeded(rows * 7919 + cols, (rows, cols))
+    d_a = a.to(dev)
+    d_b = torch.full((cols, rows), float("nan"), device=dev)
+    launch("mb_launch_transpose_2d_f32", ptr(d_a), ptr(d_b), rows, cols, None)
+    want = oracle.transpose(a.numpy())
+    assert np.array_equal(bits32(d_b), want.view(np.int32))
+
+
+def test_transpose_empty_is_noop(mb, dev):
+    d_b = torch.full((4,), 3.0, device=dev)
+    launch("mb_launch_transpose_2d_f32", ptr(d_b), ptr(d_b), 0, 4, None)
+    assert torch.all(d_b.cpu() == 3.0)
+
+
+def test_transpose_specials_bit_exact(mb, dev):
+    # NaN payloads, infinities, signed zeros and denormals move unchanged.
+    vals = np.array([np.nan, -np.nan, np.inf, -np.inf, 0.0, -0.0, 1e-45, -1e-40, 3.0],
+                    np.float32)
+    a = np.resize(vals, (96, 80)).astype(np.float32)
+    a.view(np.uint32)[5, 7] = 0x7FA00001            # signalling-NaN payload
+    d_a = torch.from_numpy(a).to(dev)
+    d_b = torch.zeros((80, 96), device=dev)
+    launch("mb_launch_transpose_2d_f32", ptr(d_a), ptr(d_b), 96, 80, None)
+    assert np.array_equal(bits32(d_b), oracle.transpose(a).view(np.int32))
+
+
+@pytest.mark.parametrize("name", ["transpose_2d", "transpose_2d_ref"])
+def test_transpose_registry_config(mb, name):
+    b, inputs, outs, _ = run_registry(name, seed=0)
+    want = oracle.transpose(inputs[0].numpy())
+    assert np.array_equal(outs[0].numpy().view(np.int32), want.view(np.int32))
