@@ -40,11 +40,11 @@ def bf16_bits_to_f64(bits: np.ndarray) -> np.ndarray:
 
 def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
     """float32 -> bf16 bit patterns, round to nearest even (NaN kept quiet)."""
-    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
-    nan = np.isnan(np.asarray(x, dtype=np.float32))
+    f = np.atleast_1d(np.asarray(x, dtype=np.float32))
+    u = f.view(np.uint32).astype(np.uint64)
     r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
-    r[nan] = 0x7FC0
-    return r
+    r[np.isnan(f)] = 0x7FC0
+    return r.reshape(np.shape(x))
 
 
 def as_f64(t) -> np.ndarray:

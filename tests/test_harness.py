@@ -1,0 +1,118 @@
+"""Harness behaviour on the CPU: gate, report text, persistence, CLI."""
+import io
+import json
+import re
+import subprocess
+import sys
+from contextlib import redirect_stdout
+
+import numpy as np
+import pytest
+
+from metalbench_amd import harness, roofline
+from metalbench_amd import helpers as H
+
+REPO = H.REPO_ROOT
+
+# Regexes of the reference's report consumers, kept verbatim in meaning:
+# agent_steel/profiler/bench_runner.py:71-83 and tests/metalbench/test_bench_accuracy_all.py:32.
+RX = {
+    "correct": re.compile(r"correctness\s+:\s*(✓\s*correct|✗\s*incorrect).*?max_err=([\d.eE+-]+)"),
+    "speedup": re.compile(r"speedup\s+:\s*([\d.eE+-]+)×"),
+    "kernel": re.compile(r"kernel\s+:\s*([\d.eE+-]+)\s*ms\s+\(min\s*([\d.eE+-]+),\s*mean\s*([\d.eE+-]+),\s*n=\d+\)"),
+    "mlx": re.compile(r"mlx\s+ref\s+:\s*([\d.eE+-]+)\s*ms"),
+    "gflops": re.compile(r"compute\s+:\s*([\d.eE+-]+)\s*GFLOPS"),
+    "gbps": re.compile(r"bandwidth\s+:\s*([\d.eE+-]+)\s*GB/s"),
+    "ai": re.compile(r"arith\s+int\.\s*:\s*([\d.eE+-]+)"),
+    "stability": re.compile(r"stability\s+:\s*([\d.eE+-]+)"),
+    "occupancy": re.compile(r"occupancy\s+:\s*tg_mem=(\d+)\s*KB\s+max_thr/tg=(\d+)"),
+    "accuracy": re.compile(r"correctness\s+:\s*(✓|✗).*?max_err=([\d.eE+-]+)"),
+}
+
+
+def _fake_result(correct=True, median=0.128):
+    chip = {"type": "gfx950", "name": "AMD Instinct MI355X", "bucket": "amd-instinct-mi355x",
+            "cpu_cores": 16, "gpu_cores": 256, "ram_bytes": 3e11}
+    k_t = {"min_ms": 0.12, "median_ms": median, "mean_ms": 0.13, "iters": 200}
+    r_t = {"min_ms": 70.0, "median_ms": 74.5, "mean_ms": 74.6, "iters": 5, "label": "cpu spec"}
+    m = {"speedup": 74.5 / median, "gflops": 0.0, "gbps": 536870912 / (median * 1e-3) / 1e9,
+         "arith_intensity": 0.0, "stability": 0.98}
+    return {"task": "transpose_2d", "chip": chip, "correct": correct, "metrics": m,
+            "kernel_timing": k_t, "reference_timing": r_t, "tg_static_mem_bytes": 16640,
+            "pso_max_threads_per_tg": 256, "outputs": [{"ok": correct, "max_err": 0.0}],
+            "compute_dtype": "f32"}
+
+
+def test_allclose_semantics():
+    ok, err = harness._allclose(np.ones(3), np.ones(4), 0, 0)
+    assert (ok, err) == (False, float("inf"))
+    assert harness._allclose(np.array([1.0, 2.0]), np.array([1.0, 2.0]), 0, 0) == (True, 0.0)
+    assert not harness._allclose(np.array([1.0, np.nan]), np.array([1.0, 2.0]), 1, 1)[0]
+    ok, err = harness._allclose(np.array([1.011]), np.array([1.0]), 1e-2, 1e-3)
+    assert ok and abs(err - 0.011) < 1e-12
+    assert not harness._allclose(np.array([1.0111]), np.array([1.0]), 1e-2, 1e-3)[0]
+
+
+def test_report_text_parses_with_reference_consumer_regexes():
+    buf = io.StringIO()
+    with redirect_stdout(buf):
+        harness._print_report(_fake_result(), "speed", 1.0)
+    out = buf.getvalue()
+    for key, rx in RX.items():
+        assert rx.search(out), f"{key} line missing:\n{out}"
+    assert RX["correct"].search(out).group(1).startswith("✓")
+    assert float(RX["kernel"].search(out).group(1)) == 0.128
+    assert "roofline    : memory-bound" in out
+    # certify's awk reads $3 of the '  kernel  ' line
+    kline = next(l for l in out.splitlines() if l.startswith("  kernel  "))
+    assert kline.split()[2] == "0.128"
+
+
+def test_session_update_rules(tmp_path):
+    sp = tmp_path / "session.json"
+    assert harness.update_session("transpose_2d", _fake_result(False), "speed", 10, sp)[0] is False
+    assert not sp.exists()
+    ok, why = harness.update_session("transpose_2d", _fake_result(True, 0.2), "speed", 10, sp)
+    assert ok and "new best" in why
+    rec = json.loads(sp.read_text())["amd-instinct-mi355x"]["transpose_2d"]
+    for key in ("best_time_ms", "speedup_vs_mlx", "gflops", "gbps", "arith_intensity", "stability",
+                "tg_static_mem_bytes", "pso_max_threads_per_tg", "iters", "target", "max_err",
+                "metal_source_path", "metal_source", "updated_at"):
+        assert key in rec
+    assert rec["metal_source_path"].endswith("transpose.hip")
+    assert harness.update_session("transpose_2d", _fake_result(True, 0.3), "speed", 10, sp)[0] is False
+    assert harness.update_session("transpose_2d", _fake_result(True, 0.1), "speed", 10, sp)[0] is True
+    md = tmp_path / "best_times.md"
+    harness._update_best_times_md(sp, md)
+    assert "transpose_2d" in md.read_text() and "0.100ms" in md.read_text()
+
+
+def test_grade_targets():
+    m = {"speedup": 2.0, "gflops": 1000.0, "gbps": 5.0, "stability": 1.0}
+    assert harness.grade(m, "speed") == 2.0
+    assert harness.grade(m, "balanced") == pytest.approx(0.5 * 2 + 0.3 * 1 + 0.2 * 1)
+    with pytest.raises(SystemExit):
+        harness.grade(m, "nope")
+
+
+def test_roofline_classification_on_mi355x_peaks():
+    t = roofline.classify("gfx950", 0, 536870912, 0.0959)
+    assert t["classification"] == "memory-bound" and t["sol"] == pytest.approx(0.70, abs=0.01)
+    g = roofline.classify("gfx950", 1_099_511_627_776, 402_653_184, 0.7282, "bf16")
+    assert g["classification"] == "compute-bound" and g["sol"] == pytest.approx(0.60, abs=0.01)
+    d = roofline.classify("gfx950", 7_516_454_912, 570_753_024, 0.07134, "bf16")
+    assert d["classification"] == "memory-bound" and d["sol"] == pytest.approx(1.0, abs=0.01)
+
+
+def test_cli_dry_run_and_cpu_only():
+    r = subprocess.run([sys.executable, "mlx/scripts/harness.py", "conv2d", "--dry-run"],
+                       cwd=REPO, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    m = json.loads(r.stdout)
+    assert m["function"] == "conv2d_f32"
+    assert [b["binding"] for b in m["buffers"]][:3] == [0, 1, 2]
+    assert {"binding": 11, "role": "scalar", "dtype": "u32", "value": 1} in m["buffers"]
+    r = subprocess.run([sys.executable, "mlx/scripts/harness.py", "sqr_mm", "--mlx-only",
+                        "--iters", "2"], cwd=REPO, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert "mlx ref     :" in r.stdout

@@ -1,0 +1,288 @@
+"""Pins the CPU oracle (oracle/) before anything is checked against it.
+
+The reference ships no golden vectors for these kernels and MLX (its
+arithmetic) is not installed, so each oracle function is pinned by checks
+that do not restate its own formula: brute-force loops, a library routine
+(torch float64 conv2d, scipy's expit, numpy complex arithmetic), closed forms
+and invariants, chosen so that a dropped term, a wrong sign/index or a
+transposed operand fails at least one of them.  A deliberately broken variant
+of the oracle is shown to fail these checks (planted mistakes, end of file)."""
+import numpy as np
+import pytest
+import scipy.special
+import torch
+
+import oracle
+
+RNG = np.random.default_rng(1234)
+
+
+def rnd(*shape):
+    return RNG.standard_normal(shape)
+
+
+# ---- bf16 conversion -----------------------------------------------------------------
+
+def test_bf16_round_trip_and_rne():
+    x = np.array([1.0, -2.5, 3.140625, 0.0, -0.0, np.inf, -np.inf], np.float32)
+    assert np.array_equal(oracle.bf16_bits_to_f64(oracle.f32_to_bf16_bits(x)), x.astype(np.float64))
+    # 1 + 2^-8 is exactly half way between bf16 neighbours 1 and 1 + 2^-7: ties to even -> 1
+    assert oracle.bf16_bits_to_f64(oracle.f32_to_bf16_bits(np.float32(1 + 2**-8)))[()] == 1.0
+    # 1 + 3*2^-8 is half way between 1 + 2^-7 and 1 + 2^-6: ties to even -> 1 + 2^-6
+    assert oracle.bf16_bits_to_f64(oracle.f32_to_bf16_bits(np.float32(1 + 3 * 2**-8)))[()] == 1 + 2**-6
+    assert np.isnan(oracle.bf16_bits_to_f64(oracle.f32_to_bf16_bits(np.float32(np.nan))))
+
+
+def test_bf16_matches_torch_conversion():
+    x = (RNG.standard_normal(10000) * 10).astype(np.float32)
+    t = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(oracle.f32_to_bf16_bits(x), t)
+
+
+# ---- transpose -------------------------------------------------------------------------
+
+def test_transpose_index_identity():
+    a = rnd(37, 53).astype(np.float32)
+    b = oracle.transpose(a)
+    assert b.shape == (53, 37)
+    for i in range(37):
+        for j in range(53):
+            assert b[j, i] == a[i, j]
+
+
+def test_transpose_involution_and_c_restatement():
+    a = rnd(129, 67).astype(np.float32)
+    assert np.array_equal(oracle.transpose(oracle.transpose(a)), a)
+    out = np.empty((67, 129), np.float32)
+    oracle.cref().oracle_transpose_f32(a.ctypes.data, out.ctypes.data, 129, 67)
+    assert np.array_equal(out, oracle.transpose(a))
+
+
+# ---- matmul ------------------------------------------------------------------------------
+
+def test_matmul_brute_force():
+    a, b = rnd(5, 7), rnd(7, 3)
+    c = oracle.matmul(a, b)
+    for i in range(5):
+        for j in range(3):
+            assert np.isclose(c[i, j], sum(a[i, p] * b[p, j] for p in range(7)), rtol=1e-13)
+
+
+def test_matmul_identity_permutation_zero():
+    a = rnd(16, 16)
+    assert np.array_equal(oracle.matmul(a, np.eye(16)), a)
+    perm = np.eye(16)[RNG.permutation(16)]
+    assert np.array_equal(oracle.matmul(perm, a), a[np.argmax(perm, axis=1)])
+    assert not oracle.matmul(a, np.zeros((16, 4))).any()
+
+
+def test_matmul_rank1_closed_form():
+    u, v, w, z = rnd(9), rnd(6), rnd(6), rnd(4)
+    got = oracle.matmul(np.outer(u, v), np.outer(w, z))
+    assert np.allclose(got, np.dot(v, w) * np.outer(u, z), rtol=1e-12, atol=1e-12)
+
+
+def test_matmul_matches_c_triple_loop():
+    a, b = rnd(33, 70), rnd(70, 41)
+    c = np.empty((33, 41))
+    oracle.cref().oracle_gemm_f64(a.ctypes.data, b.ctypes.data, c.ctypes.data, 33, 41, 70)
+    assert np.allclose(oracle.matmul(a, b), c, rtol=1e-12, atol=1e-12)
+
+
+# ---- conv2d -------------------------------------------------------------------------------
+
+def _torch_conv(x, w, stride, pad):
+    y = torch.nn.functional.conv2d(torch.from_numpy(x).permute(0, 3, 1, 2),
+                                   torch.from_numpy(w).permute(0, 3, 1, 2),
+                                   stride=stride, padding=pad)
+    return y.permute(0, 2, 3, 1).numpy()
+
+
+@pytest.mark.parametrize("n,h,w,c,o,r,s,st,pad", [
+    (2, 9, 11, 3, 4, 3, 3, 1, 1), (1, 8, 8, 5, 2, 3, 3, 1, 0), (2, 7, 6, 4, 3, 3, 3, 2, 1),
+    (1, 5, 5, 2, 2, 1, 1, 1, 0), (1, 6, 9, 3, 5, 3, 2, 1, 2),
+])
+def test_conv2d_vs_torch_and_c(n, h, w, c, o, r, s, st, pad):
+    x, wt = rnd(n, h, w, c), rnd(o, r, s, c)
+    want = _torch_conv(x, wt, st, pad)
+    got = oracle.conv2d_nhwc(x, wt, st, pad)
+    assert got.shape == want.shape
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+    yc = np.empty(want.shape)
+    oracle.cref().oracle_conv2d_nhwc_f64(x.ctypes.data, wt.ctypes.data, yc.ctypes.data,
+                                         n, h, w, c, o, r, s, st, pad)
+    assert np.allclose(got, yc, rtol=1e-12, atol=1e-12)
+
+
+def test_conv2d_1x1_is_gemm():
+    x, wt = rnd(2, 4, 5, 6), rnd(7, 1, 1, 6)
+    got = oracle.conv2d_nhwc(x, wt, 1, 0)
+    assert np.allclose(got, (x.reshape(-1, 6) @ wt.reshape(7, 6).T).reshape(2, 4, 5, 7))
+
+
+def test_conv2d_delta_kernel_is_shifted_copy():
+    # A 3x3 kernel that picks tap (r, s) = (0, 2) of channel 1 -> y[p, q] = x[p-1, q+1]
+    # (zero outside), pad 1.
+    x = rnd(1, 6, 7, 3)
+    wt = np.zeros((1, 3, 3, 3))
+    wt[0, 0, 2, 1] = 1.0
+    y = oracle.conv2d_nhwc(x, wt, 1, 1)[0, :, :, 0]
+    want = np.zeros((6, 7))
+    want[1:, :-1] = x[0, :-1, 1:, 1]
+    assert np.array_equal(y, want)
+
+
+# ---- decoder pieces ------------------------------------------------------------------------
+
+def test_rms_norm_closed_forms():
+    c = 3.0
+    x = np.full((2, 8), c)
+    assert np.allclose(oracle.rms_norm(x, 1e-5), c / np.sqrt(c * c + 1e-5))
+    y = oracle.rms_norm(rnd(4, 4096), 0.0)
+    assert np.allclose(np.sqrt(np.mean(y * y, axis=-1)), 1.0, atol=1e-12)
+
+
+def test_rope_identity_norm_composition_complex():
+    t = rnd(3, 5, 128)
+    base = 500000.0
+    assert np.allclose(oracle.rope_interleaved(t, 0, base), t)
+    r = oracle.rope_interleaved(t, 2048, base)
+    pair_norm = lambda a: a[..., 0::2] ** 2 + a[..., 1::2] ** 2  # noqa: E731
+    assert np.allclose(pair_norm(r), pair_norm(t))
+    assert np.allclose(oracle.rope_interleaved(oracle.rope_interleaved(t, 100, base), 1948, base),
+                       r, atol=1e-9)
+    # complex form: (t0 + i t1) * exp(i pos w_k), w_k = base^(-2k/Dh)
+    w = base ** (-2.0 * np.arange(64) / 128)
+    z = (t[..., 0::2] + 1j * t[..., 1::2]) * np.exp(1j * 2048 * w)
+    assert np.allclose(r[..., 0::2], z.real) and np.allclose(r[..., 1::2], z.imag)
+
+
+def test_rope_per_position_broadcast():
+    t = rnd(2, 6, 8)
+    pos = np.arange(6)[None, :]
+    r = oracle.rope_interleaved(t, pos, 10000.0)
+    for p in range(6):
+        assert np.allclose(r[:, p], oracle.rope_interleaved(t[:, p], p, 10000.0))
+
+
+def test_silu_matches_expit():
+    v = np.linspace(-30, 30, 1001)
+    assert np.allclose(oracle.silu(v), v * scipy.special.expit(v), rtol=1e-12, atol=1e-300)
+    assert oracle.silu(np.array(0.0)) == 0.0
+
+
+def test_attention_single_key_equal_keys_and_mha():
+    b, h, hkv, dh = 2, 4, 2, 16
+    q = rnd(b, h, dh)
+    empty = np.zeros((b, hkv, 0, dh))
+    k_new, v_new = rnd(b, hkv, dh), rnd(b, hkv, dh)
+    out = oracle.gqa_decode_attention(q, empty, empty, k_new, v_new)
+    assert np.allclose(out, np.repeat(v_new, h // hkv, axis=1))           # one key -> its value
+    k_same = np.repeat(k_new[:, :, None], 5, axis=2)
+    v_cache = rnd(b, hkv, 5, dh)
+    out = oracle.gqa_decode_attention(q, k_same, v_cache, k_new, v_new)
+    mean_v = (v_cache.sum(axis=2) + v_new) / 6.0                          # equal scores -> mean
+    assert np.allclose(out, np.repeat(mean_v, h // hkv, axis=1))
+    # G = 1: brute-force multi-head softmax
+    kc, vc = rnd(b, h, 7, dh), rnd(b, h, 7, dh)
+    kn, vn = rnd(b, h, dh), rnd(b, h, dh)
+    out = oracle.gqa_decode_attention(q, kc, vc, kn, vn)
+    for i in range(b):
+        for j in range(h):
+            keys = np.vstack([kc[i, j], kn[i, j]])
+            vals = np.vstack([vc[i, j], vn[i, j]])
+            s = keys @ q[i, j] / np.sqrt(dh)
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            assert np.allclose(out[i, j], p @ vals)
+
+
+def test_attention_head_maps_to_kv_head_h_div_g():
+    b, h, hkv, dh, L = 1, 8, 2, 4, 3
+    q = rnd(b, h, dh)
+    kc = rnd(b, hkv, L, dh)
+    vc = np.zeros((b, hkv, L, dh))
+    for j in range(hkv):
+        vc[:, j] = j + 1.0                       # every value of kv head j equals j + 1
+    kn = rnd(b, hkv, dh)
+    vn = np.stack([np.full((b, dh), j + 1.0) for j in range(hkv)], axis=1)
+    out = oracle.gqa_decode_attention(q, kc, vc, kn, vn)
+    for hh in range(h):
+        assert np.allclose(out[0, hh], hh // (h // hkv) + 1.0)
+
+
+def _decoder_inputs(b, d, h, hkv, ff, L, scale=0.02):
+    dh = d // h
+    return dict(x=rnd(b, d), w_qkv=rnd(d, d + 2 * hkv * dh) * scale, w_o=rnd(d, d) * scale,
+                w_gu=rnd(d, 2 * ff) * scale, w_down=rnd(ff, d) * scale,
+                k_cache=rnd(b, hkv, L, dh), v_cache=rnd(b, hkv, L, dh))
+
+
+def test_decoder_step_zero_weights_is_identity():
+    a = _decoder_inputs(2, 64, 4, 2, 96, 5)
+    for k in ("w_qkv", "w_o", "w_gu", "w_down"):
+        a[k] = np.zeros_like(a[k])
+    y, kn, vn = oracle.llama_decoder_step(**a, n_heads=4, n_kv_heads=2)
+    assert np.array_equal(y, a["x"]) and not kn.any() and not vn.any()
+
+
+def test_decoder_step_empty_cache_equals_single_token_prefill():
+    # With no cached positions the new token sits at position 0 and attends to
+    # itself only: exactly the reference's prefill layer with S = 1.
+    a = _decoder_inputs(3, 64, 4, 2, 96, 0, scale=0.1)
+    y, _, _ = oracle.llama_decoder_step(**a, n_heads=4, n_kv_heads=2, base=10000.0)
+    for i in range(3):
+        yp = oracle.llama_decoder_layer(a["x"][i:i + 1], a["w_qkv"], a["w_o"], a["w_gu"],
+                                        a["w_down"], n_heads=4, n_kv_heads=2, base=10000.0)
+        assert np.allclose(y[i], yp[0], rtol=1e-12, atol=1e-12)
+
+
+def test_decoder_step_new_key_is_rotated_projection():
+    a = _decoder_inputs(2, 64, 4, 2, 32, 6, scale=0.1)
+    _, kn, vn = oracle.llama_decoder_step(**a, n_heads=4, n_kv_heads=2)
+    h = a["x"] / np.sqrt(np.mean(a["x"] ** 2, axis=-1, keepdims=True) + 1e-5)
+    kv = h @ a["w_qkv"][:, 64:]
+    assert np.allclose(vn.reshape(2, -1), kv[:, 32:])
+    # undo the rotation with the complex conjugate at position L = 6
+    w = 500000.0 ** (-2.0 * np.arange(8) / 16)
+    z = (kn[..., 0::2] + 1j * kn[..., 1::2]) * np.exp(-1j * 6 * w)
+    k = np.empty_like(kn)
+    k[..., 0::2], k[..., 1::2] = z.real, z.imag
+    assert np.allclose(k.reshape(2, -1), kv[:, :32])
+
+
+def test_decoder_layer_zero_weights_is_identity():
+    x = rnd(8, 32)
+    z = lambda *s: np.zeros(s)  # noqa: E731
+    y = oracle.llama_decoder_layer(x, z(32, 64), z(32, 32), z(32, 96), z(48, 32),
+                                   n_heads=4, n_kv_heads=2)
+    assert np.array_equal(y, x)
+
+
+# ---- planted mistakes: the checks above must catch plausible oracle bugs -----------------
+
+def test_planted_mistakes_are_caught(monkeypatch):
+    t = rnd(1, 1, 128)
+    r = oracle.rope_interleaved(t, 5, 10000.0)
+    # wrong sign in the rotation
+    bad = r.copy()
+    bad[..., 1::2] = t[..., 0::2] * np.sin(5 * 10000.0 ** (-2 * np.arange(64) / 128)) * -1 + \
+        t[..., 1::2] * np.cos(5 * 10000.0 ** (-2 * np.arange(64) / 128))
+    w = 10000.0 ** (-2.0 * np.arange(64) / 128)
+    z = (t[..., 0::2] + 1j * t[..., 1::2]) * np.exp(1j * 5 * w)
+    assert not np.allclose(bad[..., 1::2], z.imag)
+    # transposed weight operand in conv
+    x, wt = rnd(1, 5, 5, 3), rnd(3, 3, 3, 3)
+    wrong = oracle.conv2d_nhwc(x, np.swapaxes(wt, 1, 2), 1, 1)
+    assert not np.allclose(wrong, _torch_conv(x, wt, 1, 1))
+    # GQA with head h -> kv head h % Hkv instead of h // G
+    b, h, hkv, dh = 1, 4, 2, 4
+    q = rnd(b, h, dh)
+    vc = np.stack([np.full((b, 2, dh), j + 1.0) for j in range(hkv)], axis=1)
+    kc = rnd(b, hkv, 2, dh)
+    kn = rnd(b, hkv, dh)
+    vn = vc[:, :, 0]
+    modulo = np.array([oracle.gqa_decode_attention(q[:, [hh]], kc[:, [hh % hkv]], vc[:, [hh % hkv]],
+                                                   kn[:, [hh % hkv]], vn[:, [hh % hkv]])[0, 0, 0]
+                       for hh in range(h)])
+    assert not np.allclose(modulo, [hh // (h // hkv) + 1.0 for hh in range(h)])
