@@ -241,9 +241,11 @@ typedef struct mb_decoder_step_args {
 } mb_decoder_step_args;
 
 /* Workspace bytes mb_launch_llama_decoder_step_bf16 needs for these shapes
- * (0 and mb_last_error() set if the shapes are unsupported).  The workspace
- * must be zero-filled once before its first use; the kernels leave it ready
- * for the next call.  Callable without a GPU. */
+ * (0 and mb_last_error() set if the shapes are unsupported).  A caller-owned
+ * workspace must be zero-filled before its first use and again whenever the
+ * shapes change; between calls with the same shapes the kernels leave it ready
+ * (their completion counters return to zero).  Calls sharing one workspace
+ * must not overlap.  Callable without a GPU. */
 uint64_t mb_decoder_step_workspace_bytes(const mb_decoder_step_args* args);
 
 /* Enqueue one decode step.  `args->workspace` may be NULL: the library then

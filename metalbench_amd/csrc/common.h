@@ -37,8 +37,10 @@ bool initialized();
 hipStream_t stream_or_default(void* s);   // NULL -> current library stream
 
 // Library-owned device workspace, grown on demand, freed by mb_shutdown().
-// Returns nullptr (and sets the error) on allocation failure.
-void* workspace(size_t bytes);
+// The first `zero_prefix` bytes are guaranteed zero the first time they are
+// handed out (cleared on stream `s`); the caller must leave them zero again.
+// Returns nullptr (and sets the error) on failure.
+void* library_workspace(size_t bytes, size_t zero_prefix, hipStream_t s);
 
 // ---- per-kernel timing marks ---------------------------------------------------
 // A multi-kernel entry calls mark(i, name) right before enqueuing kernel i.

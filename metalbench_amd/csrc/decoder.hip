@@ -1,12 +1,725 @@
-// placeholder translation unit; the decoder step lands here next.
+// One decode step of a LLaMA decoder layer, bf16 storage / fp32 math.
+//
+// Spec: reference mlx/kernels/full/llama_decoder_layer.py:24-64 applied to one
+// new token per sequence (see include/mbhip.h, mb_decoder_step_args):
+//   h  = x * rsqrt(mean(x^2) + eps)                              (:48-50, no gain)
+//   q|k|v = h @ W_qkv; q, k rotated by interleaved-pair RoPE at pos = L (:52-64)
+//   attn = softmax(q k^T / sqrt(Dh)) v over L cached keys + the new key,
+//          query head h reading kv head h / G                    (:30-36, mx.repeat)
+//   x1 = x + attn @ W_o                                          (:37-38)
+//   y  = x1 + (silu(h2 W_gate) * h2 W_up) @ W_down, h2 = rmsnorm(x1)   (:41-46)
+//
+// The step is HBM bound (436 MB of weights + 134 MB of KV cache per step at
+// B = 16, L = 2048 against ~7.5 GFLOP), so every kernel is shaped to stream
+// its bytes once:
+//   1. qkv_rope       skinny GEMM x @ W_qkv, finisher applies the RMSNorm row
+//                     scale (sum of squares gathered from the A operand for
+//                     free), RoPE, writes q (fp32) and k_new / v_new (bf16);
+//   2. attention      flash-decoding: one workgroup per (sequence, kv head,
+//                     128-key chunk); q.k^T on MFMA, softmax, p.v on VALU; the
+//                     last chunk to finish merges the chunks (log-sum-exp);
+//   3. wo_residual    skinny GEMM attn @ W_o, finisher adds x, writes x1
+//                     (fp32 + bf16) and per-tile sums of x1^2;
+//   4. gate_up_swiglu skinny GEMM x1 @ [W_gate | W_up], each tile holding 64
+//                     gate and the matching 64 up columns, finisher applies
+//                     the RMSNorm scale and silu(g) * u;
+//                     x1 and the SwiGLU output feed the next GEMMs as hi + lo
+//                     bf16 pairs (two MFMAs), so their bf16 rounding does not
+//                     accumulate over K = 4096 / 14336 terms;
+//   5. down_residual  skinny GEMM act @ W_down, finisher adds x1, writes y.
+// RMSNorm is a per-row scale, so (r x) W = r (x W): it is applied to the GEMM
+// outputs instead of materialising h / h2.
+//
+// Skinny GEMM (M = batch <= 16): a workgroup owns a 128-column tile and one
+// K split.  The weights are row-major [K][N] (x @ W), but the MFMA operand
+// wants 8 consecutive k per lane, so each lane loads an 8(k) x 8(n) block as
+// eight 16-byte rows (one 256-byte row segment per 16 lanes), transposes it in
+// registers with v_perm_b32 and stores eight K-contiguous 16-byte chunks into
+// LDS (pitch 136 bf16, chunk index XOR-swizzled by (row / 16) so both the
+// stores and the ds_read_b128 operand reads are bank-conflict free).  The
+// activations are the MFMA A operand (16 rows = the batch, zero-filled above
+// it), read straight from L2.  v_mfma_f32_16x16x32_bf16 accumulates; split-K
+// partials go to the workspace and the LAST workgroup of each column tile (an
+// atomic counter, reset by that workgroup) sums them and runs the epilogue.
 #include "common.h"
+
+#include <math.h>
+
+#include <algorithm>
+
 namespace mb {
-void register_decoder() {}
-}  // namespace mb
-extern "C" uint64_t mb_decoder_step_workspace_bytes(const mb_decoder_step_args*) {
-    mb::fail(MB_E_NOT_FOUND, "decoder step not built yet");
-    return 0;
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int DH = 128;        // head_dim (fixed)
+constexpr int MROWS = 16;      // MFMA rows = max batch
+constexpr int BN = 128;        // skinny GEMM column tile
+constexpr int KS = 128;        // k rows per LDS step
+constexpr int WP = KS + 8;     // LDS pitch (bf16) of one transposed weight column
+constexpr int LC = 128;        // attention keys per chunk
+constexpr int MAXG = 16;       // query heads per kv head (MFMA columns)
+constexpr int TARGET_WGS = 1024;
+
+enum { EPI_QKV = 0, EPI_WO = 1, EPI_GU = 2, EPI_DOWN = 3 };
+
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
 }
-extern "C" int mb_launch_llama_decoder_step_bf16(const mb_decoder_step_args*, void*) {
-    return mb::fail(MB_E_NOT_FOUND, "decoder step not built yet");
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
+struct StepParams {
+    uint32_t batch, d, hq, hkv, g, ff, cache_len, cache_stride, nchunks;
+    float rope_base, eps;
+    const uint16_t *x, *k_cache, *v_cache;
+    uint16_t *y, *k_new, *v_new;
+    uint32_t* attn_counters;   // [B * Hkv]
+    float* partial;            // split-K partials [tiles * splits][16][BN]
+    float* sumsq;              // [qkv tiles * splits][16] sum of x^2 over each split
+    float* q;                  // [B][D] rotated queries (fp32)
+    float* attn_part;          // [B][Hkv][nchunks][G][DH + 2]  (o[DH], m, l)
+    uint16_t* attn_out;        // [B][D]
+    float* x1;                 // [B][D]
+    uint16_t* x1b;             // [B][D]  bf16(x1)
+    uint16_t* x1b_lo;          // [B][D]  bf16(x1 - bf16(x1))
+    float* sumsq2;             // [D / 128][16] sum of x1^2 per column tile
+    uint16_t* act;             // [B][FF] bf16(silu(g) u)
+    uint16_t* act_lo;          // [B][FF] its rounding remainder
+};
+
+struct GemmCfg {
+    const uint16_t* a;     // activations [batch][k], row stride lda (rows >= batch read as 0)
+    const uint16_t* a_lo;  // optional second bf16 term of the activations (same layout)
+    uint32_t lda;
+    const uint16_t* w;     // weights [k][ldw]
+    uint32_t ldw;
+    uint32_t k, kc, splits, tiles;
+    uint32_t paired;       // 1: tile t = gate cols [64t, 64t+64) + up cols ff + [64t, 64t+64)
+    uint32_t* counters;    // [tiles]
+};
+
+__device__ __forceinline__ uint32_t tile_col(const GemmCfg& g, const StepParams& p, uint32_t tile,
+                                             uint32_t c) {
+    if (!g.paired) return tile * BN + c;
+    return c < 64 ? tile * 64 + c : p.ff + tile * 64 + (c - 64);
+}
+
+// ---- skinny GEMM + split-K finisher --------------------------------------------------
+
+template <int EPI>
+__global__ __launch_bounds__(256)
+void skinny_gemm_kernel(GemmCfg g, StepParams p) {
+    __shared__ __attribute__((aligned(16))) uint16_t wt[BN * WP];
+    float* red = reinterpret_cast<float*>(wt);   // finisher sums, after the K loop
+    __shared__ float red_ss[MROWS];
+    __shared__ uint32_t s_last;
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t tile = blockIdx.x % g.tiles;
+    const uint32_t split = blockIdx.x / g.tiles;
+    const uint32_t k_begin = split * g.kc;
+    const uint32_t nsteps = g.kc / KS;
+
+    // Loader: column octet co (16 per tile), k octet ko (16 per step).
+    const uint32_t co = tid & 15, ko = tid >> 4;
+    const uint16_t* wp = g.w + (size_t)(k_begin + 8 * ko) * g.ldw + tile_col(g, p, tile, 8 * co);
+
+    // A operand: row = lane % 16 (a sequence), k group = lane / 16.
+    const uint32_t arow = lane & 15, agrp = lane >> 4;
+    const bool arow_ok = arow < p.batch;
+    const size_t a_off = (size_t)(arow_ok ? arow : 0) * g.lda + k_begin + 8 * agrp;
+    const uint16_t* ap = g.a + a_off;
+    // GU and DOWN carry their activations as hi + lo bf16 terms (x ~ hi + lo to
+    // ~2^-16): two MFMAs per k block keep the activation rounding out of the sums.
+    constexpr bool SPLIT_A = (EPI == EPI_GU || EPI == EPI_DOWN);
+    const uint16_t* ap_lo = SPLIT_A ? g.a_lo + a_off : nullptr;
+
+    u32x4 r0[8], r1[8];
+    f32x4 acc[2] = {f32x4{}, f32x4{}};
+    float ss = 0.f;
+
+    auto load = [&](u32x4* r, uint32_t step) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            r[i] = *reinterpret_cast<const u32x4*>(wp + (size_t)(step * KS + i) * g.ldw);
+    };
+    auto compute = [&](const u32x4* r, uint32_t step) {
+        // 8x8 transpose: LDS row (8co + c) = weight column, chunk ko = k octet.
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            uint32_t lo[4], hi[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                lo[j] = __builtin_amdgcn_perm(r[2 * j + 1][m], r[2 * j][m], 0x05040100u);
+                hi[j] = __builtin_amdgcn_perm(r[2 * j + 1][m], r[2 * j][m], 0x07060302u);
+            }
+            const uint32_t row0 = 8 * co + 2 * m, row1 = row0 + 1;
+            *reinterpret_cast<u32x4*>(wt + row0 * WP + 8 * (ko ^ ((row0 >> 4) & 7))) =
+                u32x4{lo[0], lo[1], lo[2], lo[3]};
+            *reinterpret_cast<u32x4*>(wt + row1 * WP + 8 * (ko ^ ((row1 >> 4) & 7))) =
+                u32x4{hi[0], hi[1], hi[2], hi[3]};
+        }
+        __syncthreads();
+        bf16x8 a[4], alo[4];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            a[kb] = arow_ok ? *reinterpret_cast<const bf16x8*>(ap + step * KS + 32 * kb)
+                            : bf16x8{};
+            if (SPLIT_A)
+                alo[kb] = arow_ok ? *reinterpret_cast<const bf16x8*>(ap_lo + step * KS + 32 * kb)
+                                  : bf16x8{};
+            if (EPI == EPI_QKV && wave == 0) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float v = (float)a[kb][e];
+                    ss += v * v;
+                }
+            }
+        }
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            const uint32_t row = (wave * 2 + cb) * 16 + (lane & 15);
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                const uint32_t chunk = (4 * kb + agrp) ^ ((row >> 4) & 7);
+                const bf16x8 bfrag = *reinterpret_cast<const bf16x8*>(wt + row * WP + 8 * chunk);
+                acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[kb], bfrag, acc[cb], 0, 0, 0);
+                if (SPLIT_A)
+                    acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo[kb], bfrag, acc[cb], 0,
+                                                                       0, 0);
+            }
+        }
+        __syncthreads();
+    };
+
+    if (nsteps > 0) load(r0, 0);
+    for (uint32_t s = 0; s < nsteps; s += 2) {
+        if (s + 1 < nsteps) load(r1, s + 1);
+        compute(r0, s);
+        if (s + 1 < nsteps) {
+            if (s + 2 < nsteps) load(r0, s + 2);
+            compute(r1, s + 1);
+        }
+    }
+
+    // Split-K partial: lane holds rows 4*agrp + r, column (wave*2 + cb)*16 + lane%16.
+    float* part = p.partial + (size_t)(tile * g.splits + split) * MROWS * BN;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+        const uint32_t c = (wave * 2 + cb) * 16 + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part[(4 * agrp + r) * BN + c] = acc[cb][r];
+    }
+    if (EPI == EPI_QKV && wave == 0) {
+        ss += __shfl_xor(ss, 16);
+        ss += __shfl_xor(ss, 32);
+        if (lane < 16) p.sumsq[(size_t)(tile * g.splits + split) * MROWS + lane] = ss;
+    }
+
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t old = atomicAdd(&g.counters[tile], 1u);
+        s_last = (old == g.splits - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+
+    // ---- finisher: this workgroup is the last of its tile ----
+    // The fence above (agent-scope acquire) invalidated this CU's L1, so plain
+    // loads see every split's partial; they are independent and pipeline.
+    {
+        const float4* src = reinterpret_cast<const float4*>(
+            p.partial + (size_t)tile * g.splits * MROWS * BN);
+        float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+        for (uint32_t sp = 0; sp < g.splits; ++sp) {
+            const float4 a = src[(size_t)sp * (MROWS * BN / 4) + tid];
+            const float4 b = src[(size_t)sp * (MROWS * BN / 4) + 256 + tid];
+            v0.x += a.x; v0.y += a.y; v0.z += a.z; v0.w += a.w;
+            v1.x += b.x; v1.y += b.y; v1.z += b.z; v1.w += b.w;
+        }
+        reinterpret_cast<float4*>(red)[tid] = v0;
+        reinterpret_cast<float4*>(red)[256 + tid] = v1;
+    }
+    if (EPI == EPI_QKV && tid < MROWS) {
+        float v = 0.f;
+        for (uint32_t sp = 0; sp < g.splits; ++sp)
+            v += p.sumsq[(size_t)(tile * g.splits + sp) * MROWS + tid];
+        red_ss[tid] = v;
+    }
+    if (EPI == EPI_GU && tid < MROWS) {
+        float v = 0.f;
+        for (uint32_t t = 0; t < p.d / BN; ++t) v += p.sumsq2[t * MROWS + tid];
+        red_ss[tid] = rsqrtf(v / (float)p.d + p.eps);
+    }
+    __syncthreads();
+
+    if (EPI == EPI_QKV) {
+        // Tile = one head of Q, K or V (all three regions are multiples of 128).
+        const uint32_t base = tile * BN;
+        const uint32_t i = tid & 63;                       // rotation pair (2i, 2i+1)
+        const float omega = powf(p.rope_base, -2.0f * (float)i / (float)DH);
+        float sn, cs;
+        sincosf((float)p.cache_len * omega, &sn, &cs);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const uint32_t b = 4 * (tid >> 6) + rr;
+            if (b >= p.batch) continue;
+            const float r1 = rsqrtf(red_ss[b] / (float)p.d + p.eps);
+            const float v0 = red[b * BN + 2 * i] * r1, v1 = red[b * BN + 2 * i + 1] * r1;
+            if (base < p.d) {
+                float* qd = p.q + (size_t)b * p.d + base + 2 * i;
+                qd[0] = v0 * cs - v1 * sn;
+                qd[1] = v0 * sn + v1 * cs;
+            } else if (base < p.d + p.hkv * DH) {
+                const uint32_t kvh = (base - p.d) / DH;
+                uint16_t* kd = p.k_new + ((size_t)b * p.hkv + kvh) * DH + 2 * i;
+                kd[0] = f2bf(v0 * cs - v1 * sn);
+                kd[1] = f2bf(v0 * sn + v1 * cs);
+            } else {
+                const uint32_t kvh = (base - p.d - p.hkv * DH) / DH;
+                uint16_t* vd = p.v_new + ((size_t)b * p.hkv + kvh) * DH + 2 * i;
+                vd[0] = f2bf(v0);
+                vd[1] = f2bf(v1);
+            }
+        }
+    } else if (EPI == EPI_WO) {
+#pragma unroll
+        for (int i = 0; i < (MROWS * BN) / 256; ++i) {
+            const uint32_t idx = tid + 256 * i, b = idx / BN, c = idx % BN;
+            float v = 0.f;
+            if (b < p.batch) {
+                const size_t o = (size_t)b * p.d + tile * BN + c;
+                v = bf2f(p.x[o]) + red[idx];
+                p.x1[o] = v;
+                const uint16_t hi = f2bf(v);
+                p.x1b[o] = hi;
+                p.x1b_lo[o] = f2bf(v - bf2f(hi));
+            }
+            red[idx] = v * v;
+        }
+        __syncthreads();
+        if (tid < MROWS) {
+            float v = 0.f;
+            for (int c = 0; c < BN; ++c) v += red[tid * BN + c];
+            p.sumsq2[tile * MROWS + tid] = v;
+        }
+    } else if (EPI == EPI_GU) {
+#pragma unroll
+        for (int i = 0; i < (MROWS * 64) / 256; ++i) {
+            const uint32_t idx = tid + 256 * i, b = idx / 64, c = idx % 64;
+            if (b >= p.batch) continue;
+            const float r2 = red_ss[b];
+            const float gate = red[b * BN + c] * r2, up = red[b * BN + 64 + c] * r2;
+            const float av = silu(gate) * up;
+            const uint16_t hi = f2bf(av);
+            const size_t o = (size_t)b * p.ff + tile * 64 + c;
+            p.act[o] = hi;
+            p.act_lo[o] = f2bf(av - bf2f(hi));
+        }
+    } else {   // EPI_DOWN
+#pragma unroll
+        for (int i = 0; i < (MROWS * BN) / 256; ++i) {
+            const uint32_t idx = tid + 256 * i, b = idx / BN, c = idx % BN;
+            if (b >= p.batch) continue;
+            const size_t o = (size_t)b * p.d + tile * BN + c;
+            p.y[o] = f2bf(p.x1[o] + red[idx]);
+        }
+    }
+    if (tid == 0) g.counters[tile] = 0u;   // ready for the next step
+}
+
+// ---- flash-decoding attention ------------------------------------------------------------
+
+__global__ __launch_bounds__(256)
+void attention_kernel(StepParams p) {
+    __shared__ float sc[MAXG][LC + 16];        // scores, then probabilities
+    __shared__ float opart[16][4][DH];         // p.v partial sums per key group
+    __shared__ float s_m[MAXG], s_l[MAXG];
+    __shared__ uint32_t s_last;
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t G = p.g;
+    const uint32_t c = blockIdx.x % p.nchunks;
+    const uint32_t bk = blockIdx.x / p.nchunks;          // b * hkv + kvh
+    const uint32_t b = bk / p.hkv, kvh = bk - b * p.hkv;
+    const uint32_t key0 = c * LC;
+    const uint32_t ncache = p.cache_len > key0 ? min(p.cache_len - key0, (uint32_t)LC) : 0u;
+    const bool has_new = (c == p.nchunks - 1);
+    const uint32_t nkeys = ncache + (has_new ? 1u : 0u);
+    const uint32_t nkb = (nkeys + 15) / 16;
+    const uint16_t* kbase = p.k_cache + ((size_t)bk * p.cache_stride + key0) * DH;
+    const uint16_t* vbase = p.v_cache + ((size_t)bk * p.cache_stride + key0) * DH;
+    const uint16_t* knew = p.k_new + (size_t)bk * DH;
+    const uint16_t* vnew = p.v_new + (size_t)bk * DH;
+
+    // q^T as the MFMA B operand: column j = head kvh*G + j, 8 consecutive d per lane.
+    const uint32_t j = lane & 15, grp = lane >> 4;
+    const float qscale = rsqrtf((float)DH);
+    bf16x8 qf[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        bf16x8 v = {};
+        if (j < G) {
+            const float* qs = p.q + (size_t)b * p.d + (kvh * G + j) * DH + 32 * m + 8 * grp;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = (__bf16)(qs[e] * qscale);
+        }
+        qf[m] = v;
+    }
+
+    // scores S[key][head] = K q^T: A = 16 keys x 32 d, B = 32 d x 16 heads.
+    for (uint32_t kb = wave; kb < nkb; kb += 4) {
+        const uint32_t kl = kb * 16 + j;                  // key row this lane feeds
+        const uint16_t* row = kl < ncache ? kbase + (size_t)kl * DH
+                                          : (kl == ncache && has_new ? knew : nullptr);
+        f32x4 s = {};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const bf16x8 kf = row ? *reinterpret_cast<const bf16x8*>(row + 32 * m + 8 * grp)
+                                  : bf16x8{};
+            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[m], s, 0, 0, 0);
+        }
+        // lane holds S[key 4*grp + r][head j]
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t key = kb * 16 + 4 * grp + r;
+            if (j < G && key < nkeys) sc[j][key] = s[r];
+        }
+    }
+    __syncthreads();
+
+    // softmax statistics per head (one wave per head, strided)
+    for (uint32_t h = wave; h < G; h += 4) {
+        float m = -INFINITY;
+        for (uint32_t k = lane; k < nkeys; k += 64) m = fmaxf(m, sc[h][k]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        float l = 0.f;
+        for (uint32_t k = lane; k < nkeys; k += 64) {
+            const float e = expf(sc[h][k] - m);
+            sc[h][k] = e;
+            l += e;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
+        if (lane == 0) { s_m[h] = m; s_l[h] = l; }
+    }
+    __syncthreads();
+
+    // o[h][d] = sum_k p[h][k] v[k][d]: lane owns 8 d (do), key group kg strides keys.
+    const uint32_t dofs = 8 * (tid & 15), kg = tid >> 4;
+    float* out = p.attn_part + (((size_t)bk * p.nchunks + c) * G) * (DH + 2);
+    for (uint32_t h0 = 0; h0 < G; h0 += 4) {
+        float o[4][8];
+#pragma unroll
+        for (int hh = 0; hh < 4; ++hh)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[hh][e] = 0.f;
+        for (uint32_t k = kg; k < nkeys; k += 16) {
+            const uint16_t* vr = k < ncache ? vbase + (size_t)k * DH : vnew;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(vr + dofs);
+            float vf[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vf[2 * e] = __uint_as_float(v[e] << 16);
+                vf[2 * e + 1] = __uint_as_float(v[e] & 0xffff0000u);
+            }
+#pragma unroll
+            for (int hh = 0; hh < 4; ++hh) {
+                const float pr = (h0 + hh < G) ? sc[h0 + hh][k] : 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[hh][e] += pr * vf[e];
+            }
+        }
+#pragma unroll
+        for (int hh = 0; hh < 4; ++hh)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) opart[kg][hh][dofs + e] = o[hh][e];
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t idx = tid + 256 * i, hh = idx / DH, d = idx % DH;
+            if (h0 + hh < G) {
+                float v = 0.f;
+#pragma unroll
+                for (int q = 0; q < 16; ++q) v += opart[q][hh][d];
+                out[(h0 + hh) * (DH + 2) + d] = v;
+            }
+        }
+        __syncthreads();
+    }
+    if (tid < G) {
+        out[tid * (DH + 2) + DH] = s_m[tid];
+        out[tid * (DH + 2) + DH + 1] = s_l[tid];
+    }
+
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t old = atomicAdd(&p.attn_counters[bk], 1u);
+        s_last = (old == p.nchunks - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+
+    // merge the chunks of this (sequence, kv head): log-sum-exp rescaling.
+    // (The fence above invalidated L1: plain loads see the other chunks.)
+    const float* parts = p.attn_part + (size_t)bk * p.nchunks * G * (DH + 2);
+    for (uint32_t idx = tid; idx < G * DH; idx += 256) {
+        const uint32_t h = idx / DH, d = idx % DH;
+        float M = -INFINITY;
+        for (uint32_t cc = 0; cc < p.nchunks; ++cc)
+            M = fmaxf(M, parts[((size_t)cc * G + h) * (DH + 2) + DH]);
+        float L = 0.f, O = 0.f;
+        for (uint32_t cc = 0; cc < p.nchunks; ++cc) {
+            const float* pc = parts + ((size_t)cc * G + h) * (DH + 2);
+            const float w = expf(pc[DH] - M);
+            L += pc[DH + 1] * w;
+            O += pc[d] * w;
+        }
+        p.attn_out[(size_t)b * p.d + (kvh * G + h) * DH + d] = f2bf(O / L);
+    }
+    if (tid == 0) p.attn_counters[bk] = 0u;
+}
+
+// ---- host side -----------------------------------------------------------------------------
+
+struct Plan {
+    uint32_t nqkv, g, nchunks;
+    uint32_t tiles[4], splits[4];
+    size_t off_counters, off_partial, off_sumsq, off_q, off_attn_part, off_attn_out, off_x1,
+        off_x1b, off_x1b_lo, off_sumsq2, off_act, off_act_lo, total;
+    uint32_t counter_base[5];   // qkv, attn, wo, gu, down
+};
+
+static uint32_t choose_splits(uint32_t tiles, uint32_t ksteps) {
+    uint32_t best = 1;
+    for (uint32_t s = 1; s <= ksteps; ++s)
+        if (ksteps % s == 0 && (uint64_t)tiles * s <= TARGET_WGS) best = s;
+    return best;
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
+    if (!a) return fail(MB_E_ARG, "decoder step: null args");
+    if (a->batch < 1 || a->batch > MROWS)
+        return fail(MB_E_ARG, "decoder step: batch %u not in 1..%d", a->batch, MROWS);
+    if (a->head_dim != DH) return fail(MB_E_ARG, "decoder step: head_dim must be %d", DH);
+    if (a->n_heads == 0 || a->n_kv_heads == 0 || a->n_heads % a->n_kv_heads)
+        return fail(MB_E_ARG, "decoder step: n_heads %u not a multiple of n_kv_heads %u",
+                    a->n_heads, a->n_kv_heads);
+    if (a->n_heads / a->n_kv_heads > MAXG)
+        return fail(MB_E_ARG, "decoder step: more than %d query heads per kv head", MAXG);
+    if ((uint64_t)a->n_heads * DH != a->d_model)
+        return fail(MB_E_ARG, "decoder step: d_model %u != n_heads * head_dim", a->d_model);
+    if (a->d_ff == 0 || a->d_ff % KS)
+        return fail(MB_E_ARG, "decoder step: d_ff %u must be a positive multiple of %d", a->d_ff,
+                    KS);
+    if (a->cache_stride < a->cache_len)
+        return fail(MB_E_ARG, "decoder step: cache_stride %u < cache_len %u", a->cache_stride,
+                    a->cache_len);
+    if (!(a->rope_base > 0.f) || !(a->eps >= 0.f))
+        return fail(MB_E_ARG, "decoder step: rope_base must be > 0 and eps >= 0");
+    const uint32_t D = a->d_model, FF = a->d_ff, B = a->batch;
+    pl->nqkv = D + 2 * a->n_kv_heads * DH;
+    pl->g = a->n_heads / a->n_kv_heads;
+    pl->nchunks = a->cache_len == 0 ? 1u : (a->cache_len + LC - 1) / LC;
+    pl->tiles[EPI_QKV] = pl->nqkv / BN;
+    pl->tiles[EPI_WO] = D / BN;
+    pl->tiles[EPI_GU] = FF / 64;
+    pl->tiles[EPI_DOWN] = D / BN;
+    pl->splits[EPI_QKV] = choose_splits(pl->tiles[EPI_QKV], D / KS);
+    pl->splits[EPI_WO] = choose_splits(pl->tiles[EPI_WO], D / KS);
+    pl->splits[EPI_GU] = choose_splits(pl->tiles[EPI_GU], D / KS);
+    pl->splits[EPI_DOWN] = choose_splits(pl->tiles[EPI_DOWN], FF / KS);
+    size_t max_part = 0;
+    for (int i = 0; i < 4; ++i)
+        max_part = std::max(max_part, (size_t)pl->tiles[i] * pl->splits[i]);
+    const uint32_t n_counters = pl->tiles[EPI_QKV] + B * a->n_kv_heads + pl->tiles[EPI_WO] +
+                                pl->tiles[EPI_GU] + pl->tiles[EPI_DOWN];
+    pl->counter_base[0] = 0;
+    pl->counter_base[1] = pl->tiles[EPI_QKV];
+    pl->counter_base[2] = pl->counter_base[1] + B * a->n_kv_heads;
+    pl->counter_base[3] = pl->counter_base[2] + pl->tiles[EPI_WO];
+    pl->counter_base[4] = pl->counter_base[3] + pl->tiles[EPI_GU];
+    size_t o = 0;
+    pl->off_counters = o; o = align256(o + (size_t)n_counters * 4);
+    pl->off_partial = o; o = align256(o + max_part * MROWS * BN * 4);
+    pl->off_sumsq = o; o = align256(o + (size_t)pl->tiles[EPI_QKV] * pl->splits[EPI_QKV] * MROWS * 4);
+    pl->off_q = o; o = align256(o + (size_t)B * D * 4);
+    pl->off_attn_part = o;
+    o = align256(o + (size_t)B * a->n_kv_heads * pl->nchunks * pl->g * (DH + 2) * 4);
+    pl->off_attn_out = o; o = align256(o + (size_t)B * D * 2);
+    pl->off_x1 = o; o = align256(o + (size_t)B * D * 4);
+    pl->off_x1b = o; o = align256(o + (size_t)B * D * 2);
+    pl->off_x1b_lo = o; o = align256(o + (size_t)B * D * 2);
+    pl->off_sumsq2 = o; o = align256(o + (size_t)(D / BN) * MROWS * 4);
+    pl->off_act = o; o = align256(o + (size_t)B * FF * 2);
+    pl->off_act_lo = o; o = align256(o + (size_t)B * FF * 2);
+    pl->total = o;
+    return MB_OK;
+}
+
+// Only the counters must start at zero; every other region is written before
+// it is read within a step.
+static size_t counters_bytes(const Plan& pl) { return pl.off_partial; }
+
+int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) {
+    Plan pl;
+    int rc = make_plan(a, &pl);
+    if (rc) return rc;
+    if (!a->x || !a->w_qkv || !a->w_o || !a->w_gu || !a->w_down || !a->y || !a->k_new ||
+        !a->v_new || (a->cache_len && (!a->k_cache || !a->v_cache)))
+        return fail(MB_E_ARG, "decoder step: null pointer");
+    const uintptr_t align_or = (uintptr_t)a->x | (uintptr_t)a->w_qkv | (uintptr_t)a->w_o |
+                               (uintptr_t)a->w_gu | (uintptr_t)a->w_down |
+                               (uintptr_t)a->k_cache | (uintptr_t)a->v_cache;
+    if (align_or & 15) return fail(MB_E_ARG, "decoder step: inputs must be 16-byte aligned");
+
+    uint8_t* ws = static_cast<uint8_t*>(a->workspace);
+    if (ws) {
+        if (a->workspace_bytes < pl.total)
+            return fail(MB_E_ARG, "decoder step: workspace %llu bytes, need %zu",
+                        (unsigned long long)a->workspace_bytes, pl.total);
+    } else {
+        ws = static_cast<uint8_t*>(library_workspace(pl.total, counters_bytes(pl), s));
+        if (!ws) return MB_E_HIP;
+    }
+
+    StepParams p;
+    p.batch = a->batch; p.d = a->d_model; p.hq = a->n_heads; p.hkv = a->n_kv_heads; p.g = pl.g;
+    p.ff = a->d_ff; p.cache_len = a->cache_len; p.cache_stride = a->cache_stride;
+    p.nchunks = pl.nchunks; p.rope_base = a->rope_base; p.eps = a->eps;
+    p.x = a->x; p.k_cache = a->k_cache; p.v_cache = a->v_cache;
+    p.y = a->y; p.k_new = a->k_new; p.v_new = a->v_new;
+    uint32_t* counters = reinterpret_cast<uint32_t*>(ws + pl.off_counters);
+    p.attn_counters = counters + pl.counter_base[1];
+    p.partial = reinterpret_cast<float*>(ws + pl.off_partial);
+    p.sumsq = reinterpret_cast<float*>(ws + pl.off_sumsq);
+    p.q = reinterpret_cast<float*>(ws + pl.off_q);
+    p.attn_part = reinterpret_cast<float*>(ws + pl.off_attn_part);
+    p.attn_out = reinterpret_cast<uint16_t*>(ws + pl.off_attn_out);
+    p.x1 = reinterpret_cast<float*>(ws + pl.off_x1);
+    p.x1b = reinterpret_cast<uint16_t*>(ws + pl.off_x1b);
+    p.x1b_lo = reinterpret_cast<uint16_t*>(ws + pl.off_x1b_lo);
+    p.sumsq2 = reinterpret_cast<float*>(ws + pl.off_sumsq2);
+    p.act = reinterpret_cast<uint16_t*>(ws + pl.off_act);
+    p.act_lo = reinterpret_cast<uint16_t*>(ws + pl.off_act_lo);
+
+    const uint32_t D = a->d_model, FF = a->d_ff;
+    auto gemm = [&](int epi, const uint16_t* act, const uint16_t* act_lo, uint32_t lda,
+                    const uint16_t* w, uint32_t ldw, uint32_t k, uint32_t counter_base) -> GemmCfg {
+        GemmCfg g;
+        g.a = act; g.a_lo = act_lo; g.lda = lda; g.w = w; g.ldw = ldw; g.k = k;
+        g.tiles = pl.tiles[epi]; g.splits = pl.splits[epi]; g.kc = k / g.splits;
+        g.paired = epi == EPI_GU ? 1u : 0u;
+        g.counters = counters + counter_base;
+        return g;
+    };
+    const GemmCfg g_qkv =
+        gemm(EPI_QKV, a->x, nullptr, D, a->w_qkv, pl.nqkv, D, pl.counter_base[0]);
+    const GemmCfg g_wo =
+        gemm(EPI_WO, p.attn_out, nullptr, D, a->w_o, D, D, pl.counter_base[2]);
+    const GemmCfg g_gu =
+        gemm(EPI_GU, p.x1b, p.x1b_lo, D, a->w_gu, 2 * FF, D, pl.counter_base[3]);
+    const GemmCfg g_dn =
+        gemm(EPI_DOWN, p.act, p.act_lo, FF, a->w_down, D, FF, pl.counter_base[4]);
+
+    auto mark = [&](const char* name) { if (pm) pm->mark(s, name); };
+    mark("qkv_rope");
+    hipLaunchKernelGGL(skinny_gemm_kernel<EPI_QKV>, dim3(g_qkv.tiles * g_qkv.splits), dim3(256), 0,
+                       s, g_qkv, p);
+    MB_LAUNCH_CHECK("decoder qkv_rope");
+    mark("attention");
+    hipLaunchKernelGGL(attention_kernel, dim3(a->batch * a->n_kv_heads * pl.nchunks), dim3(256),
+                       0, s, p);
+    MB_LAUNCH_CHECK("decoder attention");
+    mark("wo_residual");
+    hipLaunchKernelGGL(skinny_gemm_kernel<EPI_WO>, dim3(g_wo.tiles * g_wo.splits), dim3(256), 0, s,
+                       g_wo, p);
+    MB_LAUNCH_CHECK("decoder wo_residual");
+    mark("gate_up_swiglu");
+    hipLaunchKernelGGL(skinny_gemm_kernel<EPI_GU>, dim3(g_gu.tiles * g_gu.splits), dim3(256), 0, s,
+                       g_gu, p);
+    MB_LAUNCH_CHECK("decoder gate_up_swiglu");
+    mark("down_residual");
+    hipLaunchKernelGGL(skinny_gemm_kernel<EPI_DOWN>, dim3(g_dn.tiles * g_dn.splits), dim3(256), 0,
+                       s, g_dn, p);
+    MB_LAUNCH_CHECK("decoder down_residual");
+    return MB_OK;
+}
+
+// Registry launcher (mlx/kernels/full/registry.py "llama_decoder_step"):
+// x@0 W_qkv@1 W_o@2 W_gu@3 W_down@4 K_cache@5 V_cache@6 (bf16 inputs), y@7
+// k_new@8 v_new@9 (bf16 outputs), B@10 D@11 H@12 Hkv@13 FF@14 L@15 (u32),
+// rope_base@16 eps@17 (f32).  The caches are dense: cache_stride = L.
+int run_decoder(const Bindings& bs, hipStream_t s, PartMarks* pm) {
+    uint32_t B, D, H, HKV, FF, L;
+    float base, eps;
+    int rc;
+    if ((rc = bs.u32(10, &B, "B")) || (rc = bs.u32(11, &D, "D")) || (rc = bs.u32(12, &H, "H")) ||
+        (rc = bs.u32(13, &HKV, "H_kv")) || (rc = bs.u32(14, &FF, "FF")) ||
+        (rc = bs.u32(15, &L, "L")) || (rc = bs.f32(16, &base, "rope_base")) ||
+        (rc = bs.f32(17, &eps, "eps")))
+        return rc;
+    mb_decoder_step_args a = {};
+    a.batch = B; a.d_model = D; a.n_heads = H; a.n_kv_heads = HKV; a.head_dim = DH; a.d_ff = FF;
+    a.cache_len = L; a.cache_stride = L; a.rope_base = base; a.eps = eps;
+    Plan pl;
+    if ((rc = make_plan(&a, &pl))) return rc;
+    const uint64_t nqkv = pl.nqkv, kv = (uint64_t)B * HKV * L * DH;
+    void* ptr[10];
+    if ((rc = bs.buffer(0, MB_DTYPE_BF16, (uint64_t)B * D * 2, false, &ptr[0], "x")) ||
+        (rc = bs.buffer(1, MB_DTYPE_BF16, (uint64_t)D * nqkv * 2, false, &ptr[1], "W_qkv")) ||
+        (rc = bs.buffer(2, MB_DTYPE_BF16, (uint64_t)D * D * 2, false, &ptr[2], "W_o")) ||
+        (rc = bs.buffer(3, MB_DTYPE_BF16, (uint64_t)D * 2 * FF * 2, false, &ptr[3], "W_gu")) ||
+        (rc = bs.buffer(4, MB_DTYPE_BF16, (uint64_t)FF * D * 2, false, &ptr[4], "W_down")) ||
+        (rc = bs.buffer(5, MB_DTYPE_BF16, kv * 2, false, &ptr[5], "K_cache")) ||
+        (rc = bs.buffer(6, MB_DTYPE_BF16, kv * 2, false, &ptr[6], "V_cache")) ||
+        (rc = bs.buffer(7, MB_DTYPE_BF16, (uint64_t)B * D * 2, true, &ptr[7], "y")) ||
+        (rc = bs.buffer(8, MB_DTYPE_BF16, (uint64_t)B * HKV * DH * 2, true, &ptr[8], "k_new")) ||
+        (rc = bs.buffer(9, MB_DTYPE_BF16, (uint64_t)B * HKV * DH * 2, true, &ptr[9], "v_new")))
+        return rc;
+    a.x = (const uint16_t*)ptr[0]; a.w_qkv = (const uint16_t*)ptr[1];
+    a.w_o = (const uint16_t*)ptr[2]; a.w_gu = (const uint16_t*)ptr[3];
+    a.w_down = (const uint16_t*)ptr[4]; a.k_cache = (const uint16_t*)ptr[5];
+    a.v_cache = (const uint16_t*)ptr[6]; a.y = (uint16_t*)ptr[7];
+    a.k_new = (uint16_t*)ptr[8]; a.v_new = (uint16_t*)ptr[9];
+    a.workspace = nullptr;
+    a.workspace_bytes = 0;
+    return launch_decoder(&a, s, pm);
+}
+
+}  // namespace
+
+void register_decoder() {
+    register_kernel({"llama_decoder_step_bf16", run_decoder,
+                     reinterpret_cast<const void*>(&skinny_gemm_kernel<EPI_GU>), 5});
+}
+
+}  // namespace mb
+
+extern "C" uint64_t mb_decoder_step_workspace_bytes(const mb_decoder_step_args* args) {
+    mb::clear_error();
+    mb::Plan pl;
+    if (mb::make_plan(args, &pl)) return 0;
+    return pl.total;
+}
+
+extern "C" int mb_launch_llama_decoder_step_bf16(const mb_decoder_step_args* args, void* stream) {
+    mb::clear_error();
+    if (!mb::initialized()) return mb::fail(MB_E_STATE, "mb_init() has not been called");
+    return mb::launch_decoder(args, mb::stream_or_default(stream), nullptr);
 }

@@ -21,7 +21,8 @@
 //    consecutive k per lane: each lane loads an 8(k) x 8(n) block as eight
 //    16-byte rows, transposes it in registers with 32 v_perm_b32 (pairing
 //    k and k+1 halves into dwords) and stores eight K-contiguous 16-byte rows;
-//  * global loads of stage s+1 are issued before the MFMAs of stage s;
+//  * global loads of stage s+1 are issued before the MFMAs of stage s, and
+//    the LDS operand reads of k-step kk+1 are in flight during the MFMAs of kk;
 //  * XCD-aware tile order: hardware dispatches block b to XCD b % 8, so the
 //    block id is remapped so that each XCD walks one band of GM = 4 tile-rows
 //    in column order; the 32 tiles one XCD runs at a time share 4 A panels and
@@ -35,6 +36,7 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int PITCH = BK + 8;             // bf16 per LDS row (144 B)
@@ -88,7 +90,7 @@ void gemm_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
     const uint32_t a_row = tid >> 3, a_chunk = tid & 7;
     const uint32_t b_ko = tid & 7, b_no = tid >> 3;
 
-    uint4 ra[8], rb[8];
+    u32x4 ra[8], rb[8];
 
     auto load = [&](uint32_t k0) {
 #pragma unroll
@@ -96,16 +98,15 @@ void gemm_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
             const uint32_t gm = m0 + a_row + 32 * i, gk = k0 + 8 * a_chunk;
             const uint16_t* p = A + (size_t)gm * K + gk;
             if (MODE == MODE_FULL) {
-                ra[i] = *reinterpret_cast<const uint4*>(p);
+                ra[i] = *reinterpret_cast<const u32x4*>(p);
             } else if (MODE == MODE_GUARD) {
-                ra[i] = (gm < M && gk < K) ? *reinterpret_cast<const uint4*>(p)
-                                           : make_uint4(0, 0, 0, 0);
+                ra[i] = (gm < M && gk < K) ? *reinterpret_cast<const u32x4*>(p) : u32x4{};
             } else {
                 uint16_t e[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) e[j] = (gm < M && gk + j < K) ? p[j] : (uint16_t)0;
-                ra[i] = make_uint4(e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
-                                   e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16);
+                ra[i] = u32x4{e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
+                              e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16};
             }
         }
 #pragma unroll
@@ -113,16 +114,15 @@ void gemm_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
             const uint32_t gk = k0 + 8 * b_ko + r, gn = n0 + 8 * b_no;
             const uint16_t* p = B + (size_t)gk * N + gn;
             if (MODE == MODE_FULL) {
-                rb[r] = *reinterpret_cast<const uint4*>(p);
+                rb[r] = *reinterpret_cast<const u32x4*>(p);
             } else if (MODE == MODE_GUARD) {
-                rb[r] = (gk < K && gn < N) ? *reinterpret_cast<const uint4*>(p)
-                                           : make_uint4(0, 0, 0, 0);
+                rb[r] = (gk < K && gn < N) ? *reinterpret_cast<const u32x4*>(p) : u32x4{};
             } else {
                 uint16_t e[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) e[j] = (gk < K && gn + j < N) ? p[j] : (uint16_t)0;
-                rb[r] = make_uint4(e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
-                                   e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16);
+                rb[r] = u32x4{e[0] | (uint32_t)e[1] << 16, e[2] | (uint32_t)e[3] << 16,
+                              e[4] | (uint32_t)e[5] << 16, e[6] | (uint32_t)e[7] << 16};
             }
         }
     };
@@ -132,7 +132,7 @@ void gemm_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
         uint16_t* bs = Bs + buf * TILE_ELEMS;
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            *reinterpret_cast<uint4*>(as + (a_row + 32 * i) * PITCH + 8 * a_chunk) = ra[i];
+            *reinterpret_cast<u32x4*>(as + (a_row + 32 * i) * PITCH + 8 * a_chunk) = ra[i];
         // 8x8 transpose: column c of the block = n0 + 8*no + c gets k = 8*ko .. +7.
         // Dword j of column c pairs (k = 2j, 2j+1): lo halves for even c, hi for odd.
 #pragma unroll
@@ -140,15 +140,15 @@ void gemm_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
             uint32_t lo[4], hi[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const uint32_t e = reinterpret_cast<const uint32_t*>(&rb[2 * j])[m];
-                const uint32_t o = reinterpret_cast<const uint32_t*>(&rb[2 * j + 1])[m];
+                const uint32_t e = rb[2 * j][m];
+                const uint32_t o = rb[2 * j + 1][m];
                 lo[j] = __builtin_amdgcn_perm(o, e, 0x05040100u);
                 hi[j] = __builtin_amdgcn_perm(o, e, 0x07060302u);
             }
-            *reinterpret_cast<uint4*>(bs + (8 * b_no + 2 * m) * PITCH + 8 * b_ko) =
-                make_uint4(lo[0], lo[1], lo[2], lo[3]);
-            *reinterpret_cast<uint4*>(bs + (8 * b_no + 2 * m + 1) * PITCH + 8 * b_ko) =
-                make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            *reinterpret_cast<u32x4*>(bs + (8 * b_no + 2 * m) * PITCH + 8 * b_ko) =
+                u32x4{lo[0], lo[1], lo[2], lo[3]};
+            *reinterpret_cast<u32x4*>(bs + (8 * b_no + 2 * m + 1) * PITCH + 8 * b_ko) =
+                u32x4{hi[0], hi[1], hi[2], hi[3]};
         }
     };
 
@@ -170,20 +170,28 @@ void gemm_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
         if (s + 1 < nstages) load((s + 1) * BK);
         const uint16_t* as = As + cur * TILE_ELEMS + (wm * 128 + li) * PITCH + 8 * lh;
         const uint16_t* bs = Bs + cur * TILE_ELEMS + (wn * 128 + li) * PITCH + 8 * lh;
+        // Operands of k-step kk+1 are read from LDS while the 16 MFMAs of kk run.
+        bf16x8 a[2][4], b[2][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[0][i] = *reinterpret_cast<const bf16x8*>(as + 32 * i * PITCH);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[0][j] = *reinterpret_cast<const bf16x8*>(bs + 32 * j * PITCH);
 #pragma unroll
         for (int kk = 0; kk < BK / 16; ++kk) {
-            bf16x8 a[4], b[4];
+            const int c = kk & 1;
+            if (kk + 1 < BK / 16) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                a[i] = *reinterpret_cast<const bf16x8*>(as + 32 * i * PITCH + 16 * kk);
+                for (int i = 0; i < 4; ++i)
+                    a[c ^ 1][i] = *reinterpret_cast<const bf16x8*>(as + 32 * i * PITCH + 16 * (kk + 1));
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                b[j] = *reinterpret_cast<const bf16x8*>(bs + 32 * j * PITCH + 16 * kk);
+                for (int j = 0; j < 4; ++j)
+                    b[c ^ 1][j] = *reinterpret_cast<const bf16x8*>(bs + 32 * j * PITCH + 16 * (kk + 1));
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j],
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[c][i], b[c][j], acc[i][j],
                                                                          0, 0, 0);
         }
         if (s + 1 < nstages) store(cur ^ 1);

@@ -40,6 +40,7 @@ struct State {
     hipStream_t user_stream = nullptr;
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    size_t ws_zeroed = 0;   // bytes at the front of ws known to be zero
 };
 static State g;
 
@@ -50,22 +51,38 @@ hipStream_t stream_or_default(void* s) {
     return g.user_stream ? g.user_stream : g.lib_stream;
 }
 
-void* workspace(size_t bytes) {
-    if (bytes <= g.ws_bytes) return g.ws;
-    if (g.ws) {
-        // The old workspace may still be read by enqueued work.
-        (void)hipDeviceSynchronize();
-        (void)hipFree(g.ws);
-        g.ws = nullptr;
-        g.ws_bytes = 0;
+void* library_workspace(size_t bytes, size_t zero_prefix, hipStream_t s) {
+    if (bytes > g.ws_bytes) {
+        if (g.ws) {
+            // The old workspace may still be read by enqueued work.
+            (void)hipDeviceSynchronize();
+            (void)hipFree(g.ws);
+            g.ws = nullptr;
+            g.ws_bytes = 0;
+            g.ws_zeroed = 0;
+        }
+        hipError_t e = hipMalloc(&g.ws, bytes);
+        if (e != hipSuccess) {
+            g.ws = nullptr;
+            fail(MB_E_HIP, "workspace hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+            return nullptr;
+        }
+        g.ws_bytes = bytes;
     }
-    hipError_t e = hipMalloc(&g.ws, bytes);
-    if (e != hipSuccess) {
-        g.ws = nullptr;
-        fail(MB_E_HIP, "workspace hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
-        return nullptr;
+    if (zero_prefix > g.ws_zeroed) {
+        // Counters live at the front of the workspace and are left at zero by
+        // the kernels that use them; bytes past the last caller's counters may
+        // hold its scratch data, so they are cleared (in stream order) before
+        // they serve as counters.
+        hipError_t e = hipMemsetAsync(static_cast<uint8_t*>(g.ws) + g.ws_zeroed, 0,
+                                      zero_prefix - g.ws_zeroed, s);
+        if (e != hipSuccess) {
+            fail(MB_E_HIP, "workspace clear failed: %s", hipGetErrorString(e));
+            return nullptr;
+        }
     }
-    g.ws_bytes = bytes;
+    // This caller writes non-counter data right after its own counters.
+    g.ws_zeroed = zero_prefix;
     return g.ws;
 }
 
@@ -113,7 +130,8 @@ int Bindings::buffer(uint32_t idx, uint32_t dtype, uint64_t min_bytes, bool outp
     if (b->dtype != dtype)
         return fail(MB_E_DTYPE, "binding %u (%s): dtype %s, expected %s", idx, what,
                     dtype_name(b->dtype), dtype_name(dtype));
-    if (!b->dev_ptr) return fail(MB_E_BINDING, "binding %u (%s): null pointer", idx, what);
+    if (!b->dev_ptr && min_bytes)   // an empty buffer may come with a null pointer
+        return fail(MB_E_BINDING, "binding %u (%s): null pointer", idx, what);
     if (min_bytes && b->nbytes < min_bytes)
         return fail(MB_E_BINDING, "binding %u (%s): %llu bytes, need %llu", idx, what,
                     (unsigned long long)b->nbytes, (unsigned long long)min_bytes);

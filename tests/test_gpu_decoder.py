@@ -1,0 +1,148 @@
+"""LLaMA decoder decode step on the GPU vs the float64 oracle.
+
+Gate (BASELINE): rtol 2e-2 with atol 2e-2 (outputs are O(1)), on y, k_new and
+v_new.  Covers batch 1..16, empty / short / chunk-boundary caches, GQA group
+sizes 1..8, a padded cache stride, the caller-workspace path, repeat calls
+(self-resetting split-K counters must give bit-identical results) and the full
+registry configuration."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import assert_close, run_registry, seeded
+from metalbench_amd import native
+
+pytestmark = pytest.mark.gpu
+
+RTOL = ATOL = 2e-2
+
+
+def _make(B, D, H, HKV, FF, L, stride=None, seed=0):
+    dh = 128
+    stride = stride or L
+    s = seed * 100
+    bf = "bf16"
+    ins = dict(
+        x=seeded(s + 1, (B, D), ("normal", 0.0, 1.0), bf),
+        w_qkv=seeded(s + 2, (D, D + 2 * HKV * dh), ("normal", 0.0, 0.02), bf),
+        w_o=seeded(s + 3, (D, D), ("normal", 0.0, 0.02), bf),
+        w_gu=seeded(s + 4, (D, 2 * FF), ("normal", 0.0, 0.02), bf),
+        w_down=seeded(s + 5, (FF, D), ("normal", 0.0, 0.02), bf),
+        k_cache=seeded(s + 6, (B, HKV, stride, dh), ("normal", 0.0, 1.0), bf),
+        v_cache=seeded(s + 7, (B, HKV, stride, dh), ("normal", 0.0, 1.0), bf),
+    )
+    return ins
+
+
+def _run(dev, ins, B, D, H, HKV, FF, L, stride=None, workspace=None):
+    stride = stride or L
+    d = {k: v.to(dev) for k, v in ins.items()}
+    y = torch.full((B, D), float("nan"), dtype=torch.bfloat16, device=dev)
+    kn = torch.full((B, HKV, 128), float("nan"), dtype=torch.bfloat16, device=dev)
+    vn = torch.full((B, HKV, 128), float("nan"), dtype=torch.bfloat16, device=dev)
+    a = native.MbDecoderStepArgs(
+        batch=B, d_model=D, n_heads=H, n_kv_heads=HKV, head_dim=128, d_ff=FF, cache_len=L,
+        cache_stride=stride, rope_base=500000.0, eps=1e-5,
+        x=d["x"].data_ptr(), w_qkv=d["w_qkv"].data_ptr(), w_o=d["w_o"].data_ptr(),
+        w_gu=d["w_gu"].data_ptr(), w_down=d["w_down"].data_ptr(),
+        k_cache=d["k_cache"].data_ptr(), v_cache=d["v_cache"].data_ptr(),
+        y=y.data_ptr(), k_new=kn.data_ptr(), v_new=vn.data_ptr(),
+        workspace=workspace.data_ptr() if workspace is not None else None,
+        workspace_bytes=workspace.numel() if workspace is not None else 0)
+    torch.cuda.synchronize()
+    native.check("mb_launch_llama_decoder_step_bf16",
+                 native.load().mb_launch_llama_decoder_step_bf16(ctypes.byref(a), None))
+    torch.cuda.synchronize()
+    return y.cpu(), kn.cpu(), vn.cpu()
+
+
+def _want(ins, H, HKV, L):
+    f = oracle.as_f64
+    kc = f(ins["k_cache"])[:, :, :L]
+    vc = f(ins["v_cache"])[:, :, :L]
+    return oracle.llama_decoder_step(f(ins["x"]), f(ins["w_qkv"]), f(ins["w_o"]), f(ins["w_gu"]),
+                                     f(ins["w_down"]), kc, vc, n_heads=H, n_kv_heads=HKV)
+
+
+def _check(got, want, what):
+    for g, w, name in zip(got, want, ("y", "k_new", "v_new")):
+        assert_close(oracle.as_f64(g), w, RTOL, ATOL, f"{what} {name}")
+
+
+@pytest.mark.parametrize("B,D,H,HKV,FF,L", [
+    (2, 512, 4, 2, 1024, 40),      # smoke shape
+    (1, 256, 2, 1, 384, 0),        # empty cache: attends to itself only
+    (3, 512, 4, 4, 256, 5),        # MHA (G = 1)
+    (16, 1024, 8, 1, 512, 128),    # G = 8, exactly one full chunk + the new key
+    (5, 512, 4, 2, 640, 129),      # chunk boundary + 1
+    (7, 1024, 8, 2, 1024, 300),    # three chunks, ragged
+    (16, 2048, 16, 4, 1536, 1000),  # GQA 4 as the full config, many chunks
+])
+def test_decoder_step_shapes(mb, dev, B, D, H, HKV, FF, L):
+    ins = _make(B, D, H, HKV, FF, L)
+    _check(_run(dev, ins, B, D, H, HKV, FF, L), _want(ins, H, HKV, L), f"{B,D,H,HKV,FF,L}")
+
+
+def test_decoder_step_padded_stride_and_caller_workspace(mb, dev):
+    B, D, H, HKV, FF, L, S = 4, 512, 4, 2, 512, 70, 96
+    ins = _make(B, D, H, HKV, FF, L, stride=S, seed=3)
+    a = native.MbDecoderStepArgs(batch=B, d_model=D, n_heads=H, n_kv_heads=HKV, head_dim=128,
+                                 d_ff=FF, cache_len=L, cache_stride=S, rope_base=500000.0,
+                                 eps=1e-5)
+    nbytes = native.load().mb_decoder_step_workspace_bytes(ctypes.byref(a))
+    assert nbytes > 0
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    got_ws = _run(dev, ins, B, D, H, HKV, FF, L, stride=S, workspace=ws)
+    got_lib = _run(dev, ins, B, D, H, HKV, FF, L, stride=S)
+    _check(got_ws, _want(ins, H, HKV, L), "caller workspace")
+    for g1, g2 in zip(got_ws, got_lib):
+        assert torch.equal(g1, g2)
+    # the caller's workspace is left ready: a second call gives the same bits
+    for g1, g2 in zip(got_ws, _run(dev, ins, B, D, H, HKV, FF, L, stride=S, workspace=ws)):
+        assert torch.equal(g1, g2)
+
+
+def test_decoder_step_repeat_calls_bit_identical(mb, dev):
+    B, D, H, HKV, FF, L = 16, 1024, 8, 2, 1024, 256
+    ins = _make(B, D, H, HKV, FF, L, seed=5)
+    first = _run(dev, ins, B, D, H, HKV, FF, L)
+    for _ in range(3):
+        again = _run(dev, ins, B, D, H, HKV, FF, L)
+        for g1, g2 in zip(first, again):
+            assert torch.equal(g1, g2)
+
+
+def test_decoder_step_rejects_bad_shapes(mb, dev):
+    lib = native.load()
+    a = native.MbDecoderStepArgs(batch=17, d_model=512, n_heads=4, n_kv_heads=2, head_dim=128,
+                                 d_ff=512, cache_len=4, cache_stride=4, rope_base=5e5, eps=1e-5)
+    assert lib.mb_launch_llama_decoder_step_bf16(ctypes.byref(a), None) == -7
+    a.batch, a.n_kv_heads = 4, 3
+    assert lib.mb_launch_llama_decoder_step_bf16(ctypes.byref(a), None) == -7
+    a.n_kv_heads, a.cache_stride = 2, 2
+    assert lib.mb_launch_llama_decoder_step_bf16(ctypes.byref(a), None) == -7
+
+
+def test_decoder_step_registry_config(mb):
+    """Full BASELINE config: B 16, D 4096, 32/8 heads, FF 14336, L 2048."""
+    b, inputs, outs, k_t = run_registry("llama_decoder_step", seed=0, warmup=1, iters=3)
+    f = oracle.as_f64
+    want = oracle.llama_decoder_step(*[f(t) for t in inputs], n_heads=32, n_kv_heads=8)
+    for got, w, name in zip(outs, want, ("y", "k_new", "v_new")):
+        assert_close(f(got), w, RTOL, ATOL, f"llama_decoder_step {name}")
+
+
+def test_decoder_step_library_workspace_across_shape_changes(mb, dev):
+    """Counters sit at the front of the shared library workspace; a call with
+    fewer counters writes scratch data past them, so a following call with
+    more counters must clear them first (regression test)."""
+    big = (16, 2048, 16, 4, 1536, 1000)
+    small = (4, 512, 4, 2, 512, 70)
+    mid = (16, 1024, 8, 2, 1024, 256)
+    for cfg in (big, small, mid, small, big):
+        ins = _make(*cfg, seed=7)
+        B, D, H, HKV, FF, L = cfg
+        _check(_run(dev, ins, *cfg), _want(ins, H, HKV, L), f"sequence {cfg}")
