@@ -40,7 +40,8 @@
 // activations are the MFMA A operand (16 rows = the batch, zero-filled above
 // it), read straight from L2.  v_mfma_f32_16x16x32_bf16 accumulates; split-K
 // partials go to the workspace and the LAST workgroup of each column tile (an
-// atomic counter, reset by that workgroup) sums them and runs the epilogue.
+// atomic counter, reset by that workgroup) sums them and runs the epilogue;
+// the partials travel through device-coherent (sc1) accesses, not fences.
 #include "common.h"
 
 #include <math.h>
@@ -76,16 +77,68 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
+// ---- cross-workgroup hand-off without L2 flushes ---------------------------------
+// MI355X has one L2 per XCD; an agent-scope fence (__threadfence) writes back
+// and invalidates the whole local L2, which at thousands of workgroups per
+// kernel costs more than the kernel itself.  Data one workgroup hands to
+// another inside a kernel (split-K partials, attention chunk partials) is
+// therefore written and read with device-coherent (sc1) buffer accesses, which
+// write through to / read from the coherence point, so no cached copy is ever
+// trusted:
+//   writer: sc1 stores; s_waitcnt (every store acknowledged); barrier;
+//           one relaxed agent-scope atomicAdd on the tile's counter;
+//   reader: the workgroup that brought the counter to its final value reads
+//           every partial with sc1 loads.
+constexpr int CPOL_SC1 = 16;                  // cache policy: sc1 (device coherent)
+constexpr uint32_t RSRC_FLAGS = 0x00020000u;  // buffer descriptor word 3: 32-bit data format
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, RSRC_FLAGS);
+}
+__device__ __forceinline__ void st_sc1(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, CPOL_SC1);
+}
+__device__ __forceinline__ void st_sc1(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, CPOL_SC1);
+}
+__device__ __forceinline__ f32x4 ld4_sc1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CPOL_SC1));
+}
+__device__ __forceinline__ float ld_sc1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CPOL_SC1));
+}
+
+// Signal "my sc1 stores are done" and return true in the workgroup that
+// completes `target` arrivals on `counter` (which it resets for the next use).
+__device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t target, uint32_t* s_flag) {
+    __builtin_amdgcn_s_waitcnt(0);     // this lane's sc1 stores are acknowledged
+    __syncthreads();                   // ... and every other lane's
+    if (threadIdx.x == 0) {
+        const uint32_t old =
+            __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *s_flag = (old == target - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    return *s_flag != 0u;
+}
+
+__device__ __forceinline__ void reset_counter(uint32_t* counter) {
+    if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 struct StepParams {
     uint32_t batch, d, hq, hkv, g, ff, cache_len, cache_stride, nchunks;
     float rope_base, eps;
     const uint16_t *x, *k_cache, *v_cache;
     uint16_t *y, *k_new, *v_new;
     uint32_t* attn_counters;   // [B * Hkv]
-    float* partial;            // split-K partials [tiles * splits][16][BN]
+    float* partial;            // split-K partials [tiles * splits][BN][16] (column-major tile)
+    uint32_t partial_bytes;
     float* sumsq;              // [qkv tiles * splits][16] sum of x^2 over each split
     float* q;                  // [B][D] rotated queries (fp32)
     float* attn_part;          // [B][Hkv][nchunks][G][DH + 2]  (o[DH], m, l)
+    uint32_t attn_part_bytes;
+    uint32_t sumsq_bytes;
     uint16_t* attn_out;        // [B][D]
     float* x1;                 // [B][D]
     uint16_t* x1b;             // [B][D]  bf16(x1)
@@ -210,50 +263,54 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
         }
     }
 
-    // Split-K partial: lane holds rows 4*agrp + r, column (wave*2 + cb)*16 + lane%16.
-    float* part = p.partial + (size_t)(tile * g.splits + split) * MROWS * BN;
+    // Split-K partial, column-major per tile: lane holds rows 4*agrp .. +3 of
+    // column (wave*2 + cb)*16 + lane%16 -> one 16-byte sc1 store.
+    const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(p.partial, p.partial_bytes);
+    const uint32_t part_base = (tile * g.splits + split) * (MROWS * BN * 4);
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
         const uint32_t c = (wave * 2 + cb) * 16 + (lane & 15);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) part[(4 * agrp + r) * BN + c] = acc[cb][r];
+        st_sc1(prs, part_base + (c * MROWS + 4 * agrp) * 4, acc[cb]);
     }
+    const __amdgpu_buffer_rsrc_t srs = coherent_rsrc(p.sumsq, p.sumsq_bytes);
     if (EPI == EPI_QKV && wave == 0) {
         ss += __shfl_xor(ss, 16);
         ss += __shfl_xor(ss, 32);
-        if (lane < 16) p.sumsq[(size_t)(tile * g.splits + split) * MROWS + lane] = ss;
+        if (lane < 16) st_sc1(srs, ((tile * g.splits + split) * MROWS + lane) * 4, ss);
     }
-
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t old = atomicAdd(&g.counters[tile], 1u);
-        s_last = (old == g.splits - 1) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+    if (!arrive_last(&g.counters[tile], g.splits, &s_last)) return;
 
     // ---- finisher: this workgroup is the last of its tile ----
-    // The fence above (agent-scope acquire) invalidated this CU's L1, so plain
-    // loads see every split's partial; they are independent and pipeline.
+    // float4 q of a tile = column q/4, rows 4*(q%4) .. +3; sum over the splits.
     {
-        const float4* src = reinterpret_cast<const float4*>(
-            p.partial + (size_t)tile * g.splits * MROWS * BN);
-        float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
-        for (uint32_t sp = 0; sp < g.splits; ++sp) {
-            const float4 a = src[(size_t)sp * (MROWS * BN / 4) + tid];
-            const float4 b = src[(size_t)sp * (MROWS * BN / 4) + 256 + tid];
-            v0.x += a.x; v0.y += a.y; v0.z += a.z; v0.w += a.w;
-            v1.x += b.x; v1.y += b.y; v1.z += b.z; v1.w += b.w;
+        const uint32_t tile_base = tile * g.splits * (MROWS * BN * 4);
+        f32x4 v0 = {}, v1 = {};
+        uint32_t sp = 0;
+        for (; sp + 2 <= g.splits; sp += 2) {
+            const uint32_t o0 = tile_base + sp * (MROWS * BN * 4), o1 = o0 + MROWS * BN * 4;
+            const f32x4 a0 = ld4_sc1(prs, o0 + tid * 16), b0 = ld4_sc1(prs, o0 + (256 + tid) * 16);
+            const f32x4 a1 = ld4_sc1(prs, o1 + tid * 16), b1 = ld4_sc1(prs, o1 + (256 + tid) * 16);
+            v0 += a0 + a1;
+            v1 += b0 + b1;
         }
-        reinterpret_cast<float4*>(red)[tid] = v0;
-        reinterpret_cast<float4*>(red)[256 + tid] = v1;
+        if (sp < g.splits) {
+            const uint32_t o0 = tile_base + sp * (MROWS * BN * 4);
+            v0 += ld4_sc1(prs, o0 + tid * 16);
+            v1 += ld4_sc1(prs, o0 + (256 + tid) * 16);
+        }
+        // red is row-major [16][BN] for the epilogues
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t q = tid + 256 * h, c = q >> 2, r0 = 4 * (q & 3);
+            const f32x4 v = h ? v1 : v0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) red[(r0 + e) * BN + c] = v[e];
+        }
     }
     if (EPI == EPI_QKV && tid < MROWS) {
         float v = 0.f;
         for (uint32_t sp = 0; sp < g.splits; ++sp)
-            v += p.sumsq[(size_t)(tile * g.splits + sp) * MROWS + tid];
+            v += ld_sc1(srs, ((tile * g.splits + sp) * MROWS + tid) * 4);
         red_ss[tid] = v;
     }
     if (EPI == EPI_GU && tid < MROWS) {
@@ -335,7 +392,7 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
             p.y[o] = f2bf(p.x1[o] + red[idx]);
         }
     }
-    if (tid == 0) g.counters[tile] = 0u;   // ready for the next step
+    reset_counter(&g.counters[tile]);   // ready for the next step
 }
 
 // ---- flash-decoding attention ------------------------------------------------------------
@@ -418,7 +475,8 @@ void attention_kernel(StepParams p) {
 
     // o[h][d] = sum_k p[h][k] v[k][d]: lane owns 8 d (do), key group kg strides keys.
     const uint32_t dofs = 8 * (tid & 15), kg = tid >> 4;
-    float* out = p.attn_part + (((size_t)bk * p.nchunks + c) * G) * (DH + 2);
+    const __amdgpu_buffer_rsrc_t ars = coherent_rsrc(p.attn_part, p.attn_part_bytes);
+    const uint32_t out_base = ((bk * p.nchunks + c) * G) * (DH + 2) * 4;
     for (uint32_t h0 = 0; h0 < G; h0 += 4) {
         float o[4][8];
 #pragma unroll
@@ -453,44 +511,34 @@ void attention_kernel(StepParams p) {
                 float v = 0.f;
 #pragma unroll
                 for (int q = 0; q < 16; ++q) v += opart[q][hh][d];
-                out[(h0 + hh) * (DH + 2) + d] = v;
+                st_sc1(ars, out_base + ((h0 + hh) * (DH + 2) + d) * 4, v);
             }
         }
         __syncthreads();
     }
     if (tid < G) {
-        out[tid * (DH + 2) + DH] = s_m[tid];
-        out[tid * (DH + 2) + DH + 1] = s_l[tid];
+        st_sc1(ars, out_base + (tid * (DH + 2) + DH) * 4, s_m[tid]);
+        st_sc1(ars, out_base + (tid * (DH + 2) + DH + 1) * 4, s_l[tid]);
     }
+    if (!arrive_last(&p.attn_counters[bk], p.nchunks, &s_last)) return;
 
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t old = atomicAdd(&p.attn_counters[bk], 1u);
-        s_last = (old == p.nchunks - 1) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-
-    // merge the chunks of this (sequence, kv head): log-sum-exp rescaling.
-    // (The fence above invalidated L1: plain loads see the other chunks.)
-    const float* parts = p.attn_part + (size_t)bk * p.nchunks * G * (DH + 2);
+    // merge the chunks of this (sequence, kv head): log-sum-exp rescaling
+    const uint32_t parts = bk * p.nchunks * G * (DH + 2) * 4;
     for (uint32_t idx = tid; idx < G * DH; idx += 256) {
         const uint32_t h = idx / DH, d = idx % DH;
         float M = -INFINITY;
         for (uint32_t cc = 0; cc < p.nchunks; ++cc)
-            M = fmaxf(M, parts[((size_t)cc * G + h) * (DH + 2) + DH]);
+            M = fmaxf(M, ld_sc1(ars, parts + ((cc * G + h) * (DH + 2) + DH) * 4));
         float L = 0.f, O = 0.f;
         for (uint32_t cc = 0; cc < p.nchunks; ++cc) {
-            const float* pc = parts + ((size_t)cc * G + h) * (DH + 2);
-            const float w = expf(pc[DH] - M);
-            L += pc[DH + 1] * w;
-            O += pc[d] * w;
+            const uint32_t pc = parts + (cc * G + h) * (DH + 2) * 4;
+            const float w = expf(ld_sc1(ars, pc + DH * 4) - M);
+            L += ld_sc1(ars, pc + (DH + 1) * 4) * w;
+            O += ld_sc1(ars, pc + d * 4) * w;
         }
         p.attn_out[(size_t)b * p.d + (kvh * G + h) * DH + d] = f2bf(O / L);
     }
-    if (tid == 0) p.attn_counters[bk] = 0u;
+    reset_counter(&p.attn_counters[bk]);
 }
 
 // ---- host side -----------------------------------------------------------------------------
@@ -569,6 +617,9 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
     pl->off_act = o; o = align256(o + (size_t)B * FF * 2);
     pl->off_act_lo = o; o = align256(o + (size_t)B * FF * 2);
     pl->total = o;
+    if (pl->off_attn_out - pl->off_attn_part > 0x7fffffffull ||
+        pl->off_sumsq - pl->off_partial > 0x7fffffffull)
+        return fail(MB_E_ARG, "decoder step: shapes too large for 32-bit workspace offsets");
     return MB_OK;
 }
 
@@ -607,6 +658,9 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
     uint32_t* counters = reinterpret_cast<uint32_t*>(ws + pl.off_counters);
     p.attn_counters = counters + pl.counter_base[1];
     p.partial = reinterpret_cast<float*>(ws + pl.off_partial);
+    p.partial_bytes = (uint32_t)(pl.off_sumsq - pl.off_partial);
+    p.sumsq_bytes = (uint32_t)(pl.off_q - pl.off_sumsq);
+    p.attn_part_bytes = (uint32_t)(pl.off_attn_out - pl.off_attn_part);
     p.sumsq = reinterpret_cast<float*>(ws + pl.off_sumsq);
     p.q = reinterpret_cast<float*>(ws + pl.off_q);
     p.attn_part = reinterpret_cast<float*>(ws + pl.off_attn_part);
