@@ -14,9 +14,10 @@
 // its bytes once:
 //   1. qkv_rope       skinny GEMM x @ W_qkv, finisher applies the RMSNorm row
 //                     scale (sum of squares gathered from the A operand for
-//                     free), RoPE, writes q (fp32) and k_new / v_new (bf16);
+//                     free), RoPE, writes q (bf16, pre-scaled by 1/sqrt(Dh))
+//                     and k_new / v_new (bf16);
 //   2. attention      flash-decoding: one workgroup per (sequence, kv head,
-//                     128-key chunk); q.k^T on MFMA, softmax, p.v on VALU; the
+//                     64-key chunk); q.k^T on MFMA, softmax, p.v on VALU; the
 //                     last chunk to finish merges the chunks (log-sum-exp);
 //   3. wo_residual    skinny GEMM attn @ W_o, finisher adds x, writes x1
 //                     (fp32 + bf16) and per-tile sums of x1^2;
@@ -60,7 +61,7 @@ constexpr int MROWS = 16;      // MFMA rows = max batch
 constexpr int BN = 128;        // skinny GEMM column tile
 constexpr int KS = 128;        // k rows per LDS step
 constexpr int WP = KS + 8;     // LDS pitch (bf16) of one transposed weight column
-constexpr int LC = 128;        // attention keys per chunk
+constexpr int LC = 64;         // attention keys per chunk (one 16-key block per wave)
 constexpr int MAXG = 16;       // query heads per kv head (MFMA columns)
 constexpr int TARGET_WGS = 1024;
 
@@ -135,7 +136,7 @@ struct StepParams {
     float* partial;            // split-K partials [tiles * splits][BN][16] (column-major tile)
     uint32_t partial_bytes;
     float* sumsq;              // [qkv tiles * splits][16] sum of x^2 over each split
-    float* q;                  // [B][D] rotated queries (fp32)
+    uint16_t* q;               // [B][D] rotated queries * 1/sqrt(Dh), bf16 (MFMA operand)
     float* attn_part;          // [B][Hkv][nchunks][G][DH + 2]  (o[DH], m, l)
     uint32_t attn_part_bytes;
     uint32_t sumsq_bytes;
@@ -281,22 +282,28 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
     if (!arrive_last(&g.counters[tile], g.splits, &s_last)) return;
 
     // ---- finisher: this workgroup is the last of its tile ----
-    // float4 q of a tile = column q/4, rows 4*(q%4) .. +3; sum over the splits.
+    // float4 q of a tile = column q/4, rows 4*(q%4) .. +3; sum over the splits,
+    // eight splits (16 loads) in flight per lane.
     {
-        const uint32_t tile_base = tile * g.splits * (MROWS * BN * 4);
+        constexpr uint32_t SPLIT_BYTES = MROWS * BN * 4;
+        const uint32_t tile_base = tile * g.splits * SPLIT_BYTES;
         f32x4 v0 = {}, v1 = {};
         uint32_t sp = 0;
-        for (; sp + 2 <= g.splits; sp += 2) {
-            const uint32_t o0 = tile_base + sp * (MROWS * BN * 4), o1 = o0 + MROWS * BN * 4;
-            const f32x4 a0 = ld4_sc1(prs, o0 + tid * 16), b0 = ld4_sc1(prs, o0 + (256 + tid) * 16);
-            const f32x4 a1 = ld4_sc1(prs, o1 + tid * 16), b1 = ld4_sc1(prs, o1 + (256 + tid) * 16);
-            v0 += a0 + a1;
-            v1 += b0 + b1;
+        for (; sp + 8 <= g.splits; sp += 8) {
+            f32x4 a[8], b[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t o = tile_base + (sp + u) * SPLIT_BYTES;
+                a[u] = ld4_sc1(prs, o + tid * 16);
+                b[u] = ld4_sc1(prs, o + (256 + tid) * 16);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) { v0 += a[u]; v1 += b[u]; }
         }
-        if (sp < g.splits) {
-            const uint32_t o0 = tile_base + sp * (MROWS * BN * 4);
-            v0 += ld4_sc1(prs, o0 + tid * 16);
-            v1 += ld4_sc1(prs, o0 + (256 + tid) * 16);
+        for (; sp < g.splits; ++sp) {
+            const uint32_t o = tile_base + sp * SPLIT_BYTES;
+            v0 += ld4_sc1(prs, o + tid * 16);
+            v1 += ld4_sc1(prs, o + (256 + tid) * 16);
         }
         // red is row-major [16][BN] for the epilogues
 #pragma unroll
@@ -334,9 +341,11 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
             const float r1 = rsqrtf(red_ss[b] / (float)p.d + p.eps);
             const float v0 = red[b * BN + 2 * i] * r1, v1 = red[b * BN + 2 * i + 1] * r1;
             if (base < p.d) {
-                float* qd = p.q + (size_t)b * p.d + base + 2 * i;
-                qd[0] = v0 * cs - v1 * sn;
-                qd[1] = v0 * sn + v1 * cs;
+                // pre-scaled by 1/sqrt(Dh) and rounded once for the q.k^T MFMA
+                const float qs = rsqrtf((float)DH);
+                uint16_t* qd = p.q + (size_t)b * p.d + base + 2 * i;
+                qd[0] = f2bf((v0 * cs - v1 * sn) * qs);
+                qd[1] = f2bf((v0 * sn + v1 * cs) * qs);
             } else if (base < p.d + p.hkv * DH) {
                 const uint32_t kvh = (base - p.d) / DH;
                 uint16_t* kd = p.k_new + ((size_t)b * p.hkv + kvh) * DH + 2 * i;
@@ -396,11 +405,22 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
 }
 
 // ---- flash-decoding attention ------------------------------------------------------------
+// One workgroup per (sequence, kv head, 64-key chunk); the last chunk also
+// holds the new token's key/value.  Every K/V load of the chunk is issued at
+// the start (32 KB per workgroup in flight), then:
+//   scores  S = K q^T on MFMA (A = 16 keys x 32 d, B = 32 d x 16 query heads),
+//   softmax per head (one wave per head),
+//   o = p v on VALU: lane owns 8 d and a group of keys, reduced across the
+//   key groups with lane shuffles and a 8 KB LDS pass,
+// and the chunk's (o, max, sum) go out as sc1 partials; the workgroup that
+// completes the (sequence, kv head) merges the chunks with log-sum-exp.
+
+constexpr int KEYS_PER_THREAD = (LC + 16) / 16;   // key slots of the p.v loop (incl. the new key)
 
 __global__ __launch_bounds__(256)
 void attention_kernel(StepParams p) {
     __shared__ float sc[MAXG][LC + 16];        // scores, then probabilities
-    __shared__ float opart[16][4][DH];         // p.v partial sums per key group
+    __shared__ float opart[4][4][DH];          // per-wave p.v partial sums
     __shared__ float s_m[MAXG], s_l[MAXG];
     __shared__ uint32_t s_last;
 
@@ -413,49 +433,58 @@ void attention_kernel(StepParams p) {
     const uint32_t ncache = p.cache_len > key0 ? min(p.cache_len - key0, (uint32_t)LC) : 0u;
     const bool has_new = (c == p.nchunks - 1);
     const uint32_t nkeys = ncache + (has_new ? 1u : 0u);
-    const uint32_t nkb = (nkeys + 15) / 16;
+    const uint32_t nkb = (nkeys + 15) / 16;                 // <= LC/16 + 1
     const uint16_t* kbase = p.k_cache + ((size_t)bk * p.cache_stride + key0) * DH;
     const uint16_t* vbase = p.v_cache + ((size_t)bk * p.cache_stride + key0) * DH;
     const uint16_t* knew = p.k_new + (size_t)bk * DH;
     const uint16_t* vnew = p.v_new + (size_t)bk * DH;
+    auto key_row = [&](const uint16_t* cache, const uint16_t* fresh, uint32_t k) -> const uint16_t* {
+        return k < ncache ? cache + (size_t)k * DH : (k == ncache && has_new ? fresh : nullptr);
+    };
 
-    // q^T as the MFMA B operand: column j = head kvh*G + j, 8 consecutive d per lane.
+    // ---- issue every load of the chunk ----
     const uint32_t j = lane & 15, grp = lane >> 4;
-    const float qscale = rsqrtf((float)DH);
-    bf16x8 qf[4];
+    bf16x8 kf[2][4];                                       // key blocks wave, wave + 4
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        bf16x8 v = {};
-        if (j < G) {
-            const float* qs = p.q + (size_t)b * p.d + (kvh * G + j) * DH + 32 * m + 8 * grp;
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t kb = wave + 4 * i;
+        const uint16_t* row = kb < nkb ? key_row(kbase, knew, kb * 16 + j) : nullptr;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = (__bf16)(qs[e] * qscale);
-        }
-        qf[m] = v;
+        for (int m = 0; m < 4; ++m)
+            kf[i][m] = row ? *reinterpret_cast<const bf16x8*>(row + 32 * m + 8 * grp) : bf16x8{};
     }
+    const uint32_t dofs = 8 * (tid & 15), kg = tid >> 4;   // p.v: 8 d per lane, key group kg
+    u32x4 vr[KEYS_PER_THREAD];
+#pragma unroll
+    for (int i = 0; i < KEYS_PER_THREAD; ++i) {
+        const uint16_t* row = key_row(vbase, vnew, kg + 16 * i);
+        vr[i] = row ? *reinterpret_cast<const u32x4*>(row + dofs) : u32x4{};
+    }
+    bf16x8 qf[4];                                          // q^T: column j = head kvh*G + j
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+        qf[m] = j < G ? *reinterpret_cast<const bf16x8*>(
+                            p.q + (size_t)b * p.d + (kvh * G + j) * DH + 32 * m + 8 * grp)
+                      : bf16x8{};
 
-    // scores S[key][head] = K q^T: A = 16 keys x 32 d, B = 32 d x 16 heads.
-    for (uint32_t kb = wave; kb < nkb; kb += 4) {
-        const uint32_t kl = kb * 16 + j;                  // key row this lane feeds
-        const uint16_t* row = kl < ncache ? kbase + (size_t)kl * DH
-                                          : (kl == ncache && has_new ? knew : nullptr);
+    // ---- scores ----
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t kb = wave + 4 * i;
+        if (kb >= nkb) break;
         f32x4 s = {};
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const bf16x8 kf = row ? *reinterpret_cast<const bf16x8*>(row + 32 * m + 8 * grp)
-                                  : bf16x8{};
-            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[m], s, 0, 0, 0);
-        }
-        // lane holds S[key 4*grp + r][head j]
+        for (int m = 0; m < 4; ++m)
+            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[i][m], qf[m], s, 0, 0, 0);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < 4; ++r) {                      // lane holds S[key 4*grp + r][head j]
             const uint32_t key = kb * 16 + 4 * grp + r;
             if (j < G && key < nkeys) sc[j][key] = s[r];
         }
     }
     __syncthreads();
 
-    // softmax statistics per head (one wave per head, strided)
+    // ---- softmax statistics per head ----
     for (uint32_t h = wave; h < G; h += 4) {
         float m = -INFINITY;
         for (uint32_t k = lane; k < nkeys; k += 64) m = fmaxf(m, sc[h][k]);
@@ -473,8 +502,7 @@ void attention_kernel(StepParams p) {
     }
     __syncthreads();
 
-    // o[h][d] = sum_k p[h][k] v[k][d]: lane owns 8 d (do), key group kg strides keys.
-    const uint32_t dofs = 8 * (tid & 15), kg = tid >> 4;
+    // ---- o = p v ----
     const __amdgpu_buffer_rsrc_t ars = coherent_rsrc(p.attn_part, p.attn_part_bytes);
     const uint32_t out_base = ((bk * p.nchunks + c) * G) * (DH + 2) * 4;
     for (uint32_t h0 = 0; h0 < G; h0 += 4) {
@@ -483,14 +511,15 @@ void attention_kernel(StepParams p) {
         for (int hh = 0; hh < 4; ++hh)
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[hh][e] = 0.f;
-        for (uint32_t k = kg; k < nkeys; k += 16) {
-            const uint16_t* vr = k < ncache ? vbase + (size_t)k * DH : vnew;
-            const u32x4 v = *reinterpret_cast<const u32x4*>(vr + dofs);
+#pragma unroll
+        for (int i = 0; i < KEYS_PER_THREAD; ++i) {
+            const uint32_t k = kg + 16 * i;
+            if (k >= nkeys) break;
             float vf[8];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                vf[2 * e] = __uint_as_float(v[e] << 16);
-                vf[2 * e + 1] = __uint_as_float(v[e] & 0xffff0000u);
+                vf[2 * e] = __uint_as_float(vr[i][e] << 16);
+                vf[2 * e + 1] = __uint_as_float(vr[i][e] & 0xffff0000u);
             }
 #pragma unroll
             for (int hh = 0; hh < 4; ++hh) {
@@ -499,18 +528,29 @@ void attention_kernel(StepParams p) {
                 for (int e = 0; e < 8; ++e) o[hh][e] += pr * vf[e];
             }
         }
+        // lanes l, l^16, l^32, l^48 share dofs: fold the wave's four key groups
 #pragma unroll
         for (int hh = 0; hh < 4; ++hh)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) opart[kg][hh][dofs + e] = o[hh][e];
+            for (int e = 0; e < 8; ++e) {
+                float v = o[hh][e];
+                v += __shfl_xor(v, 16);
+                v += __shfl_xor(v, 32);
+                o[hh][e] = v;
+            }
+        if (lane < 16) {
+#pragma unroll
+            for (int hh = 0; hh < 4; ++hh)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) opart[wave][hh][dofs + e] = o[hh][e];
+        }
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const uint32_t idx = tid + 256 * i, hh = idx / DH, d = idx % DH;
             if (h0 + hh < G) {
-                float v = 0.f;
-#pragma unroll
-                for (int q = 0; q < 16; ++q) v += opart[q][hh][d];
+                const float v = opart[0][hh][d] + opart[1][hh][d] + opart[2][hh][d] +
+                                opart[3][hh][d];
                 st_sc1(ars, out_base + ((h0 + hh) * (DH + 2) + d) * 4, v);
             }
         }
@@ -522,19 +562,43 @@ void attention_kernel(StepParams p) {
     }
     if (!arrive_last(&p.attn_counters[bk], p.nchunks, &s_last)) return;
 
-    // merge the chunks of this (sequence, kv head): log-sum-exp rescaling
+    // ---- merge the chunks of this (sequence, kv head): log-sum-exp rescaling ----
+    // Loads are batched eight chunks at a time so they are in flight together.
     const uint32_t parts = bk * p.nchunks * G * (DH + 2) * 4;
+    constexpr uint32_t U = 8;
     for (uint32_t idx = tid; idx < G * DH; idx += 256) {
         const uint32_t h = idx / DH, d = idx % DH;
+        auto at = [&](uint32_t cc, uint32_t e) { return parts + ((cc * G + h) * (DH + 2) + e) * 4; };
         float M = -INFINITY;
-        for (uint32_t cc = 0; cc < p.nchunks; ++cc)
-            M = fmaxf(M, ld_sc1(ars, parts + ((cc * G + h) * (DH + 2) + DH) * 4));
+        uint32_t cc = 0;
+        for (; cc + U <= p.nchunks; cc += U) {
+            float m[U];
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) m[u] = ld_sc1(ars, at(cc + u, DH));
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) M = fmaxf(M, m[u]);
+        }
+        for (; cc < p.nchunks; ++cc) M = fmaxf(M, ld_sc1(ars, at(cc, DH)));
         float L = 0.f, O = 0.f;
-        for (uint32_t cc = 0; cc < p.nchunks; ++cc) {
-            const uint32_t pc = parts + (cc * G + h) * (DH + 2) * 4;
-            const float w = expf(ld_sc1(ars, pc + DH * 4) - M);
-            L += ld_sc1(ars, pc + (DH + 1) * 4) * w;
-            O += ld_sc1(ars, pc + d * 4) * w;
+        for (cc = 0; cc + U <= p.nchunks; cc += U) {
+            float m[U], l[U], o[U];
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) {
+                m[u] = ld_sc1(ars, at(cc + u, DH));
+                l[u] = ld_sc1(ars, at(cc + u, DH + 1));
+                o[u] = ld_sc1(ars, at(cc + u, d));
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) {
+                const float w = expf(m[u] - M);
+                L += l[u] * w;
+                O += o[u] * w;
+            }
+        }
+        for (; cc < p.nchunks; ++cc) {
+            const float w = expf(ld_sc1(ars, at(cc, DH)) - M);
+            L += ld_sc1(ars, at(cc, DH + 1)) * w;
+            O += ld_sc1(ars, at(cc, d)) * w;
         }
         p.attn_out[(size_t)b * p.d + (kvh * G + h) * DH + d] = f2bf(O / L);
     }
@@ -606,7 +670,7 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
     pl->off_counters = o; o = align256(o + (size_t)n_counters * 4);
     pl->off_partial = o; o = align256(o + max_part * MROWS * BN * 4);
     pl->off_sumsq = o; o = align256(o + (size_t)pl->tiles[EPI_QKV] * pl->splits[EPI_QKV] * MROWS * 4);
-    pl->off_q = o; o = align256(o + (size_t)B * D * 4);
+    pl->off_q = o; o = align256(o + (size_t)B * D * 2);
     pl->off_attn_part = o;
     o = align256(o + (size_t)B * a->n_kv_heads * pl->nchunks * pl->g * (DH + 2) * 4);
     pl->off_attn_out = o; o = align256(o + (size_t)B * D * 2);
@@ -662,7 +726,7 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
     p.sumsq_bytes = (uint32_t)(pl.off_q - pl.off_sumsq);
     p.attn_part_bytes = (uint32_t)(pl.off_attn_out - pl.off_attn_part);
     p.sumsq = reinterpret_cast<float*>(ws + pl.off_sumsq);
-    p.q = reinterpret_cast<float*>(ws + pl.off_q);
+    p.q = reinterpret_cast<uint16_t*>(ws + pl.off_q);
     p.attn_part = reinterpret_cast<float*>(ws + pl.off_attn_part);
     p.attn_out = reinterpret_cast<uint16_t*>(ws + pl.off_attn_out);
     p.x1 = reinterpret_cast<float*>(ws + pl.off_x1);
