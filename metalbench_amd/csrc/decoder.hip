@@ -63,7 +63,6 @@ constexpr int KS = 128;        // k rows per LDS step
 constexpr int WP = KS + 8;     // LDS pitch (bf16) of one transposed weight column
 constexpr int LC = 64;         // attention keys per chunk (one 16-key block per wave)
 constexpr int MAXG = 16;       // query heads per kv head (MFMA columns)
-constexpr int TARGET_WGS = 1024;
 
 enum { EPI_QKV = 0, EPI_WO = 1, EPI_GU = 2, EPI_DOWN = 3 };
 
@@ -168,10 +167,29 @@ __device__ __forceinline__ uint32_t tile_col(const GemmCfg& g, const StepParams&
 
 // ---- skinny GEMM + split-K finisher --------------------------------------------------
 
-template <int EPI>
-__global__ __launch_bounds__(256)
+// A workgroup owns one 128-column tile and one K split of NSTEPS x 128 rows
+// (NSTEPS = 1, 2 or 4).  The step is HBM bound with long memory latency under
+// load, so what matters is bytes in flight per CU:
+//   1. the split's activation slice (16 rows x NSTEPS*128, hi and lo terms) is
+//      loaded first and parked in LDS, so the MFMA A fragments come from LDS
+//      (lgkmcnt) and never sit in the vmcnt queue ahead of weight data;
+//   2. then ALL of the split's weight loads are issued at once (NSTEPS x 32 KB
+//      per workgroup, two workgroups per CU);
+//   3. step s waits only for its own weight rows (vmcnt = 8 x steps still in
+//      flight behind them), transposes them through LDS and runs its MFMAs.
+// sched_barrier keeps the compiler from interleaving these groups, because
+// vmcnt retires loads in issue order.
+template <int EPI, int NSTEPS>
+__global__ __launch_bounds__(256, 2)
 void skinny_gemm_kernel(GemmCfg g, StepParams p) {
+    constexpr bool SPLIT_A = (EPI == EPI_GU || EPI == EPI_DOWN);   // hi + lo activations
+    constexpr int NTERMS = SPLIT_A ? 2 : 1;
+    constexpr int KC = NSTEPS * KS;                 // k rows of this split
+    constexpr int AP = KC + 8;                      // LDS pitch (bf16) of an activation row
+    constexpr int ACH = MROWS * KC / 8 / 256;       // 16-byte activation chunks per thread per term
+
     __shared__ __attribute__((aligned(16))) uint16_t wt[BN * WP];
+    __shared__ __attribute__((aligned(16))) uint16_t as[NTERMS][MROWS * AP];
     float* red = reinterpret_cast<float*>(wt);   // finisher sums, after the K loop
     __shared__ float red_ss[MROWS];
     __shared__ uint32_t s_last;
@@ -179,41 +197,63 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t tile = blockIdx.x % g.tiles;
     const uint32_t split = blockIdx.x / g.tiles;
-    const uint32_t k_begin = split * g.kc;
-    const uint32_t nsteps = g.kc / KS;
+    const uint32_t k_begin = split * KC;
 
-    // Loader: column octet co (16 per tile), k octet ko (16 per step).
+    // ---- 1. activations -> registers (issued first) ----
+    // chunk q (0 .. 16*KC/8): row q / (KC/8), k octet q % (KC/8)
+    u32x4 ar[NTERMS][ACH];
+#pragma unroll
+    for (int t = 0; t < NTERMS; ++t) {
+        const uint16_t* src = t == 0 ? g.a : g.a_lo;
+#pragma unroll
+        for (int i = 0; i < ACH; ++i) {
+            const uint32_t q = tid + 256 * i, row = q / (KC / 8), oct = q % (KC / 8);
+            const bool ok = row < p.batch;
+            // rows past the batch read row 0 (valid) and are zeroed
+            const u32x4 v = *reinterpret_cast<const u32x4*>(
+                src + (size_t)(ok ? row : 0) * g.lda + k_begin + 8 * oct);
+            ar[t][i] = ok ? v : u32x4{};
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 2. every weight load of the split ----
     const uint32_t co = tid & 15, ko = tid >> 4;
     const uint16_t* wp = g.w + (size_t)(k_begin + 8 * ko) * g.ldw + tile_col(g, p, tile, 8 * co);
+    u32x4 r[NSTEPS][8];
+#pragma unroll
+    for (int s = 0; s < NSTEPS; ++s)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            r[s][i] = *reinterpret_cast<const u32x4*>(wp + (size_t)(s * KS + i) * g.ldw);
+    __builtin_amdgcn_sched_barrier(0);
 
-    // A operand: row = lane % 16 (a sequence), k group = lane / 16.
+    // ---- activations -> LDS (they are the oldest loads) ----
+#pragma unroll
+    for (int t = 0; t < NTERMS; ++t)
+#pragma unroll
+        for (int i = 0; i < ACH; ++i) {
+            const uint32_t q = tid + 256 * i, row = q / (KC / 8), oct = q % (KC / 8);
+            *reinterpret_cast<u32x4*>(&as[t][row * AP + 8 * oct]) = ar[t][i];
+        }
+    __builtin_amdgcn_sched_barrier(0);
+
     const uint32_t arow = lane & 15, agrp = lane >> 4;
-    const bool arow_ok = arow < p.batch;
-    const size_t a_off = (size_t)(arow_ok ? arow : 0) * g.lda + k_begin + 8 * agrp;
-    const uint16_t* ap = g.a + a_off;
-    // GU and DOWN carry their activations as hi + lo bf16 terms (x ~ hi + lo to
-    // ~2^-16): two MFMAs per k block keep the activation rounding out of the sums.
-    constexpr bool SPLIT_A = (EPI == EPI_GU || EPI == EPI_DOWN);
-    const uint16_t* ap_lo = SPLIT_A ? g.a_lo + a_off : nullptr;
-
-    u32x4 r0[8], r1[8];
     f32x4 acc[2] = {f32x4{}, f32x4{}};
     float ss = 0.f;
 
-    auto load = [&](u32x4* r, uint32_t step) {
+    // ---- 3. steps ----
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            r[i] = *reinterpret_cast<const u32x4*>(wp + (size_t)(step * KS + i) * g.ldw);
-    };
-    auto compute = [&](const u32x4* r, uint32_t step) {
-        // 8x8 transpose: LDS row (8co + c) = weight column, chunk ko = k octet.
+    for (int s = 0; s < NSTEPS; ++s) {
+        // 8x8 transpose of this lane's block: LDS row (8co + c) = weight
+        // column, 16-byte chunk ko (XOR-swizzled by row/16) = k octet.
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
             uint32_t lo[4], hi[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                lo[j] = __builtin_amdgcn_perm(r[2 * j + 1][m], r[2 * j][m], 0x05040100u);
-                hi[j] = __builtin_amdgcn_perm(r[2 * j + 1][m], r[2 * j][m], 0x07060302u);
+                lo[j] = __builtin_amdgcn_perm(r[s][2 * j + 1][m], r[s][2 * j][m], 0x05040100u);
+                hi[j] = __builtin_amdgcn_perm(r[s][2 * j + 1][m], r[s][2 * j][m], 0x07060302u);
             }
             const uint32_t row0 = 8 * co + 2 * m, row1 = row0 + 1;
             *reinterpret_cast<u32x4*>(wt + row0 * WP + 8 * (ko ^ ((row0 >> 4) & 7))) =
@@ -225,18 +265,9 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
         bf16x8 a[4], alo[4];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            a[kb] = arow_ok ? *reinterpret_cast<const bf16x8*>(ap + step * KS + 32 * kb)
-                            : bf16x8{};
-            if (SPLIT_A)
-                alo[kb] = arow_ok ? *reinterpret_cast<const bf16x8*>(ap_lo + step * KS + 32 * kb)
-                                  : bf16x8{};
-            if (EPI == EPI_QKV && wave == 0) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float v = (float)a[kb][e];
-                    ss += v * v;
-                }
-            }
+            const uint32_t ao = arow * AP + s * KS + 32 * kb + 8 * agrp;
+            a[kb] = *reinterpret_cast<const bf16x8*>(&as[0][ao]);
+            if (SPLIT_A) alo[kb] = *reinterpret_cast<const bf16x8*>(&as[NTERMS - 1][ao]);
         }
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
@@ -251,17 +282,16 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
                                                                        0, 0);
             }
         }
-        __syncthreads();
-    };
-
-    if (nsteps > 0) load(r0, 0);
-    for (uint32_t s = 0; s < nsteps; s += 2) {
-        if (s + 1 < nsteps) load(r1, s + 1);
-        compute(r0, s);
-        if (s + 1 < nsteps) {
-            if (s + 2 < nsteps) load(r0, s + 2);
-            compute(r1, s + 1);
+        if (EPI == EPI_QKV && wave == 0) {   // RMSNorm statistics from the A operand
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float v = (float)a[kb][e];
+                    ss += v * v;
+                }
         }
+        __syncthreads();
     }
 
     // Split-K partial, column-major per tile: lane holds rows 4*agrp .. +3 of
@@ -438,35 +468,45 @@ void attention_kernel(StepParams p) {
     const uint16_t* vbase = p.v_cache + ((size_t)bk * p.cache_stride + key0) * DH;
     const uint16_t* knew = p.k_new + (size_t)bk * DH;
     const uint16_t* vnew = p.v_new + (size_t)bk * DH;
+    // Row of key k of the chunk, or the new token's row as a harmless stand-in
+    // for k past the chunk (the value is then zeroed by a select, so every load
+    // is unconditional and the waitcnt pass sees the exact load order).
     auto key_row = [&](const uint16_t* cache, const uint16_t* fresh, uint32_t k) -> const uint16_t* {
-        return k < ncache ? cache + (size_t)k * DH : (k == ncache && has_new ? fresh : nullptr);
+        return k < ncache ? cache + (size_t)k * DH : fresh;
     };
+    auto key_ok = [&](uint32_t k) { return k < nkeys; };
 
     // ---- issue every load of the chunk ----
     const uint32_t j = lane & 15, grp = lane >> 4;
+    bf16x8 qf[4];                                          // q^T: column j = head kvh*G + j
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+    {
+        // heads past G read head 0 (valid) and are zeroed
+        const bf16x8 v = *reinterpret_cast<const bf16x8*>(
+            p.q + (size_t)b * p.d + (kvh * G + (j < G ? j : 0)) * DH + 32 * m + 8 * grp);
+        qf[m] = j < G ? v : bf16x8{};
+    }
+
     bf16x8 kf[2][4];                                       // key blocks wave, wave + 4
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const uint32_t kb = wave + 4 * i;
-        const uint16_t* row = kb < nkb ? key_row(kbase, knew, kb * 16 + j) : nullptr;
+        const uint32_t k = (wave + 4 * i) * 16 + j;
+        const uint16_t* row = key_row(kbase, knew, k);
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
-            kf[i][m] = row ? *reinterpret_cast<const bf16x8*>(row + 32 * m + 8 * grp) : bf16x8{};
+        for (int m = 0; m < 4; ++m) {
+            const bf16x8 v = *reinterpret_cast<const bf16x8*>(row + 32 * m + 8 * grp);
+            kf[i][m] = key_ok(k) ? v : bf16x8{};
+        }
     }
     const uint32_t dofs = 8 * (tid & 15), kg = tid >> 4;   // p.v: 8 d per lane, key group kg
     u32x4 vr[KEYS_PER_THREAD];
 #pragma unroll
     for (int i = 0; i < KEYS_PER_THREAD; ++i) {
-        const uint16_t* row = key_row(vbase, vnew, kg + 16 * i);
-        vr[i] = row ? *reinterpret_cast<const u32x4*>(row + dofs) : u32x4{};
+        const uint32_t k = kg + 16 * i;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(key_row(vbase, vnew, k) + dofs);
+        vr[i] = key_ok(k) ? v : u32x4{};
     }
-    bf16x8 qf[4];                                          // q^T: column j = head kvh*G + j
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-        qf[m] = j < G ? *reinterpret_cast<const bf16x8*>(
-                            p.q + (size_t)b * p.d + (kvh * G + j) * DH + 32 * m + 8 * grp)
-                      : bf16x8{};
-
     // ---- scores ----
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -615,11 +655,10 @@ struct Plan {
     uint32_t counter_base[5];   // qkv, attn, wo, gu, down
 };
 
-static uint32_t choose_splits(uint32_t tiles, uint32_t ksteps) {
-    uint32_t best = 1;
-    for (uint32_t s = 1; s <= ksteps; ++s)
-        if (ksteps % s == 0 && (uint64_t)tiles * s <= TARGET_WGS) best = s;
-    return best;
+// Steps per K split: 4 (128 KB of weights in flight per workgroup) when the
+// K range divides, else 2 or 1.
+static uint32_t choose_steps(uint32_t ksteps) {
+    return ksteps % 4 == 0 ? 4u : (ksteps % 2 == 0 ? 2u : 1u);
 }
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -652,10 +691,10 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
     pl->tiles[EPI_WO] = D / BN;
     pl->tiles[EPI_GU] = FF / 64;
     pl->tiles[EPI_DOWN] = D / BN;
-    pl->splits[EPI_QKV] = choose_splits(pl->tiles[EPI_QKV], D / KS);
-    pl->splits[EPI_WO] = choose_splits(pl->tiles[EPI_WO], D / KS);
-    pl->splits[EPI_GU] = choose_splits(pl->tiles[EPI_GU], D / KS);
-    pl->splits[EPI_DOWN] = choose_splits(pl->tiles[EPI_DOWN], FF / KS);
+    pl->splits[EPI_QKV] = (D / KS) / choose_steps(D / KS);
+    pl->splits[EPI_WO] = (D / KS) / choose_steps(D / KS);
+    pl->splits[EPI_GU] = (D / KS) / choose_steps(D / KS);
+    pl->splits[EPI_DOWN] = (FF / KS) / choose_steps(FF / KS);
     size_t max_part = 0;
     for (int i = 0; i < 4; ++i)
         max_part = std::max(max_part, (size_t)pl->tiles[i] * pl->splits[i]);
@@ -690,6 +729,16 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
 // Only the counters must start at zero; every other region is written before
 // it is read within a step.
 static size_t counters_bytes(const Plan& pl) { return pl.off_partial; }
+
+template <int EPI>
+void launch_skinny(const GemmCfg& g, const StepParams& p, hipStream_t s) {
+    const dim3 grid(g.tiles * g.splits), block(256);
+    switch (g.kc / KS) {
+        case 1: hipLaunchKernelGGL((skinny_gemm_kernel<EPI, 1>), grid, block, 0, s, g, p); break;
+        case 2: hipLaunchKernelGGL((skinny_gemm_kernel<EPI, 2>), grid, block, 0, s, g, p); break;
+        default: hipLaunchKernelGGL((skinny_gemm_kernel<EPI, 4>), grid, block, 0, s, g, p); break;
+    }
+}
 
 int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) {
     Plan pl;
@@ -757,24 +806,20 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
 
     auto mark = [&](const char* name) { if (pm) pm->mark(s, name); };
     mark("qkv_rope");
-    hipLaunchKernelGGL(skinny_gemm_kernel<EPI_QKV>, dim3(g_qkv.tiles * g_qkv.splits), dim3(256), 0,
-                       s, g_qkv, p);
+    launch_skinny<EPI_QKV>(g_qkv, p, s);
     MB_LAUNCH_CHECK("decoder qkv_rope");
     mark("attention");
     hipLaunchKernelGGL(attention_kernel, dim3(a->batch * a->n_kv_heads * pl.nchunks), dim3(256),
                        0, s, p);
     MB_LAUNCH_CHECK("decoder attention");
     mark("wo_residual");
-    hipLaunchKernelGGL(skinny_gemm_kernel<EPI_WO>, dim3(g_wo.tiles * g_wo.splits), dim3(256), 0, s,
-                       g_wo, p);
+    launch_skinny<EPI_WO>(g_wo, p, s);
     MB_LAUNCH_CHECK("decoder wo_residual");
     mark("gate_up_swiglu");
-    hipLaunchKernelGGL(skinny_gemm_kernel<EPI_GU>, dim3(g_gu.tiles * g_gu.splits), dim3(256), 0, s,
-                       g_gu, p);
+    launch_skinny<EPI_GU>(g_gu, p, s);
     MB_LAUNCH_CHECK("decoder gate_up_swiglu");
     mark("down_residual");
-    hipLaunchKernelGGL(skinny_gemm_kernel<EPI_DOWN>, dim3(g_dn.tiles * g_dn.splits), dim3(256), 0,
-                       s, g_dn, p);
+    launch_skinny<EPI_DOWN>(g_dn, p, s);
     MB_LAUNCH_CHECK("decoder down_residual");
     return MB_OK;
 }
@@ -824,7 +869,7 @@ int run_decoder(const Bindings& bs, hipStream_t s, PartMarks* pm) {
 
 void register_decoder() {
     register_kernel({"llama_decoder_step_bf16", run_decoder,
-                     reinterpret_cast<const void*>(&skinny_gemm_kernel<EPI_GU>), 5});
+                     reinterpret_cast<const void*>(&skinny_gemm_kernel<EPI_GU, 4>), 5});
 }
 
 }  // namespace mb
