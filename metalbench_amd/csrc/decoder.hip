@@ -61,7 +61,6 @@ constexpr int MROWS = 16;      // MFMA rows = max batch
 constexpr int BN = 128;        // skinny GEMM column tile
 constexpr int KS = 128;        // k rows per LDS step
 constexpr int WP = KS + 8;     // LDS pitch (bf16) of one transposed weight column
-constexpr int LC = 64;         // attention keys per chunk (one 16-key block per wave)
 constexpr int MAXG = 16;       // query heads per kv head (MFMA columns)
 
 enum { EPI_QKV = 0, EPI_WO = 1, EPI_GU = 2, EPI_DOWN = 3 };
@@ -127,7 +126,7 @@ __device__ __forceinline__ void reset_counter(uint32_t* counter) {
 }
 
 struct StepParams {
-    uint32_t batch, d, hq, hkv, g, ff, cache_len, cache_stride, nchunks;
+    uint32_t batch, d, hq, hkv, g, ff, cache_len, cache_stride, nsplit, split_keys;
     float rope_base, eps;
     const uint16_t *x, *k_cache, *v_cache;
     uint16_t *y, *k_new, *v_new;
@@ -136,7 +135,7 @@ struct StepParams {
     uint32_t partial_bytes;
     float* sumsq;              // [qkv tiles * splits][16] sum of x^2 over each split
     uint16_t* q;               // [B][D] rotated queries * 1/sqrt(Dh), bf16 (MFMA operand)
-    float* attn_part;          // [B][Hkv][nchunks][G][DH + 2]  (o[DH], m, l)
+    float* attn_part;          // [B][Hkv][nsplit][G][DH + 4]  (o[DH], m, l, pad)
     uint32_t attn_part_bytes;
     uint32_t sumsq_bytes;
     uint16_t* attn_out;        // [B][D]
@@ -435,212 +434,267 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
 }
 
 // ---- flash-decoding attention ------------------------------------------------------------
-// One workgroup per (sequence, kv head, 64-key chunk); the last chunk also
-// holds the new token's key/value.  Every K/V load of the chunk is issued at
-// the start (32 KB per workgroup in flight), then:
+// The cached keys of each (sequence, kv head) are cut into `nsplit` splits of
+// `split_keys` keys; one workgroup streams one split, 64 keys per iteration,
+// wave w taking the 16-key block at offset 16 w.  Each wave runs its own
+// online softmax, with the next block's K and V loads in flight while the
+// current block is computed (register double buffer, no workgroup barrier in
+// the loop):
 //   scores  S = K q^T on MFMA (A = 16 keys x 32 d, B = 32 d x 16 query heads),
-//   softmax per head (one wave per head),
-//   o = p v on VALU: lane owns 8 d and a group of keys, reduced across the
-//   key groups with lane shuffles and a 8 KB LDS pass,
-// and the chunk's (o, max, sum) go out as sc1 partials; the workgroup that
-// completes the (sequence, kv head) merges the chunks with log-sum-exp.
+//           lane (j, grp) holds S[key 4 grp + r][head j], r < 4;
+//   softmax running max / sum per head, folded over the four lanes of a head
+//           with lane shuffles;
+//   o = p v on VALU: lane l owns d = 2l, 2l + 1 of every key (one dword per
+//           key row, so each V load is one whole 256-byte row per wave); the
+//           block's probabilities reach it through a wave-private LDS slot.
+// K and V are read through buffer descriptors clipped at the split's last
+// key: loads past it return zeros without touching memory, so every load is
+// unconditional and the waitcnt pass sees one fixed load order.  The four
+// waves are combined through LDS and the split's unnormalised (o, max, sum)
+// go out as sc1 partials.  The workgroup that completes the (sequence, kv
+// head) merges the splits and the new token (key and value from k_new /
+// v_new) with log-sum-exp weights; all its partial loads are issued
+// together, so the merge costs one memory round trip.
 
-constexpr int KEYS_PER_THREAD = (LC + 16) / 16;   // key slots of the p.v loop (incl. the new key)
+constexpr int AKEYS = 64;                 // keys per workgroup iteration
+constexpr int APITCH = DH + 4;            // floats per (split, head) partial: o[DH], m, l, pad
+constexpr int QP = DH + 8;                // LDS pitch (bf16) of a query row
+constexpr float NEG_BIG = -1.0e30f;       // "no key yet": finite, so max/exp never see inf - inf
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr uint32_t ATTN_WGS = 1024;      // attention grid target: 4 workgroups per CU
 
+__device__ __forceinline__ void* uniform_ptr(const void* ptr) {
+    const uint64_t v = reinterpret_cast<uint64_t>(ptr);
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<void*>((hi << 32) | lo);
+}
+
+struct KVBlock {
+    u32x4 k[4];      // K[key j][32 m + 8 grp .. + 8] for the scores MFMA, m < 4
+    uint32_t v[16];  // V[key i][2 lane, 2 lane + 1], i < 16
+};
+
+template <int GT>
 __global__ __launch_bounds__(256)
 void attention_kernel(StepParams p) {
-    __shared__ float sc[MAXG][LC + 16];        // scores, then probabilities
-    __shared__ float opart[4][4][DH];          // per-wave p.v partial sums
-    __shared__ float s_m[MAXG], s_l[MAXG];
+    __shared__ uint16_t qs[16][QP];        // q rows of this kv head (rows past G zero)
+    __shared__ float xp[4][16][16];       // per wave: p[key][head] of the current block
+    __shared__ float xa[4][4][16];        // per wave: rescale factor of each head (row 0 read)
+    __shared__ float wo[4][GT][DH];       // per wave: o after the key loop
+    __shared__ float wm[4][GT], wl[4][GT];
+    __shared__ float s_new[GT];
     __shared__ uint32_t s_last;
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t j = lane & 15, grp = lane >> 4;
     const uint32_t G = p.g;
-    const uint32_t c = blockIdx.x % p.nchunks;
-    const uint32_t bk = blockIdx.x / p.nchunks;          // b * hkv + kvh
+    const uint32_t split = blockIdx.x % p.nsplit;
+    const uint32_t bk = blockIdx.x / p.nsplit;            // b * hkv + kvh
     const uint32_t b = bk / p.hkv, kvh = bk - b * p.hkv;
-    const uint32_t key0 = c * LC;
-    const uint32_t ncache = p.cache_len > key0 ? min(p.cache_len - key0, (uint32_t)LC) : 0u;
-    const bool has_new = (c == p.nchunks - 1);
-    const uint32_t nkeys = ncache + (has_new ? 1u : 0u);
-    const uint32_t nkb = (nkeys + 15) / 16;                 // <= LC/16 + 1
-    const uint16_t* kbase = p.k_cache + ((size_t)bk * p.cache_stride + key0) * DH;
-    const uint16_t* vbase = p.v_cache + ((size_t)bk * p.cache_stride + key0) * DH;
+    const uint32_t key0 = split * p.split_keys;
+    const uint32_t key_end = min(key0 + p.split_keys, p.cache_len);
+    const uint32_t nkeys = key_end > key0 ? key_end - key0 : 0u;
+    const uint32_t nblk = (nkeys + AKEYS - 1) / AKEYS;
+    const size_t row0 = (size_t)bk * p.cache_stride + key0;
+    // (the descriptors are workgroup-uniform; readfirstlane lets the compiler
+    // keep them in SGPRs instead of wrapping each load in a waterfall loop)
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(nkeys ? p.k_cache + row0 * DH : p.k_new), 0,
+        __builtin_amdgcn_readfirstlane(nkeys * DH * 2), RSRC_FLAGS);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(nkeys ? p.v_cache + row0 * DH : p.v_new), 0,
+        __builtin_amdgcn_readfirstlane(nkeys * DH * 2), RSRC_FLAGS);
     const uint16_t* knew = p.k_new + (size_t)bk * DH;
     const uint16_t* vnew = p.v_new + (size_t)bk * DH;
-    // Row of key k of the chunk, or the new token's row as a harmless stand-in
-    // for k past the chunk (the value is then zeroed by a select, so every load
-    // is unconditional and the waitcnt pass sees the exact load order).
-    auto key_row = [&](const uint16_t* cache, const uint16_t* fresh, uint32_t k) -> const uint16_t* {
-        return k < ncache ? cache + (size_t)k * DH : fresh;
-    };
-    auto key_ok = [&](uint32_t k) { return k < nkeys; };
 
-    // ---- issue every load of the chunk ----
-    const uint32_t j = lane & 15, grp = lane >> 4;
-    bf16x8 qf[4];                                          // q^T: column j = head kvh*G + j
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-    {
-        // heads past G read head 0 (valid) and are zeroed
-        const bf16x8 v = *reinterpret_cast<const bf16x8*>(
-            p.q + (size_t)b * p.d + (kvh * G + (j < G ? j : 0)) * DH + 32 * m + 8 * grp);
-        qf[m] = j < G ? v : bf16x8{};
-    }
-
-    bf16x8 kf[2][4];                                       // key blocks wave, wave + 4
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const uint32_t k = (wave + 4 * i) * 16 + j;
-        const uint16_t* row = key_row(kbase, knew, k);
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const bf16x8 v = *reinterpret_cast<const bf16x8*>(row + 32 * m + 8 * grp);
-            kf[i][m] = key_ok(k) ? v : bf16x8{};
-        }
-    }
-    const uint32_t dofs = 8 * (tid & 15), kg = tid >> 4;   // p.v: 8 d per lane, key group kg
-    u32x4 vr[KEYS_PER_THREAD];
-#pragma unroll
-    for (int i = 0; i < KEYS_PER_THREAD; ++i) {
-        const uint32_t k = kg + 16 * i;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(key_row(vbase, vnew, k) + dofs);
-        vr[i] = key_ok(k) ? v : u32x4{};
-    }
-    // ---- scores ----
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const uint32_t kb = wave + 4 * i;
-        if (kb >= nkb) break;
-        f32x4 s = {};
+    // Offsets (bytes) inside the split of this lane's first K and V dwords.
+    const uint32_t koff = ((16 * wave + j) * DH + 8 * grp) * 2;
+    const uint32_t voff = ((16 * wave) * DH + 2 * lane) * 2;
+    auto load = [&](KVBlock& blk, uint32_t t) {
+        const uint32_t base = t * AKEYS * DH * 2;
 #pragma unroll
         for (int m = 0; m < 4; ++m)
-            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[i][m], qf[m], s, 0, 0, 0);
+            blk.k[m] = __builtin_amdgcn_raw_buffer_load_b128(krs, base + koff + 64 * m, 0, 0);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {                      // lane holds S[key 4*grp + r][head j]
-            const uint32_t key = kb * 16 + 4 * grp + r;
-            if (j < G && key < nkeys) sc[j][key] = s[r];
-        }
-    }
+        for (int i = 0; i < 16; ++i)
+            blk.v[i] = __builtin_amdgcn_raw_buffer_load_b32(vrs, base + voff + i * DH * 2, 0, 0);
+    };
+
+    // q rows of the G heads go to LDS (the MFMA B operand is re-read per
+    // block); their loads are issued ahead of the first K/V block.
+    static_assert(16 * (DH / 8) == 256, "one 16-byte q chunk per thread");
+    const uint32_t qh = tid / (DH / 8), qc = tid % (DH / 8);
+    const u32x4 qv = *reinterpret_cast<const u32x4*>(
+        p.q + (size_t)b * p.d + (kvh * G + (qh < G ? qh : 0)) * DH + 8 * qc);
+    KVBlock ba, bb;
+    load(ba, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    *reinterpret_cast<u32x4*>(&qs[qh][8 * qc]) = qh < G ? qv : u32x4{};
     __syncthreads();
 
-    // ---- softmax statistics per head ----
-    for (uint32_t h = wave; h < G; h += 4) {
-        float m = -INFINITY;
-        for (uint32_t k = lane; k < nkeys; k += 64) m = fmaxf(m, sc[h][k]);
+    float m_run = NEG_BIG, l_run = 0.f;   // lane (j, grp): head j; l over this lane's keys
+    float o[GT][2];                       // lane: o[h][d = 2 lane + e]
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-        float l = 0.f;
-        for (uint32_t k = lane; k < nkeys; k += 64) {
-            const float e = expf(sc[h][k] - m);
-            sc[h][k] = e;
-            l += e;
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
-        if (lane == 0) { s_m[h] = m; s_l[h] = l; }
-    }
-    __syncthreads();
+    for (int h = 0; h < GT; ++h) o[h][0] = o[h][1] = 0.f;
 
-    // ---- o = p v ----
-    const __amdgpu_buffer_rsrc_t ars = coherent_rsrc(p.attn_part, p.attn_part_bytes);
-    const uint32_t out_base = ((bk * p.nchunks + c) * G) * (DH + 2) * 4;
-    for (uint32_t h0 = 0; h0 < G; h0 += 4) {
-        float o[4][8];
+    auto compute = [&](const KVBlock& blk, uint32_t t) {
+        const uint32_t kb = t * AKEYS + 16 * wave;     // block's first key, relative to key0
+        f32x4 s = {};
 #pragma unroll
-        for (int hh = 0; hh < 4; ++hh)
+        for (int m = 0; m < 4; ++m) {
+            const bf16x8 qv = *reinterpret_cast<const bf16x8*>(&qs[j][32 * m + 8 * grp]);
+            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, blk.k[m]), qv,
+                                                        s, 0, 0, 0);
+        }
+        float mloc = NEG_BIG;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o[hh][e] = 0.f;
+        for (int r = 0; r < 4; ++r)
+            if (kb + 4 * grp + r < nkeys) mloc = fmaxf(mloc, s[r]);
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+        const float m_new = fmaxf(m_run, mloc);
+        const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * LOG2E);
+        float pr[4];
 #pragma unroll
-        for (int i = 0; i < KEYS_PER_THREAD; ++i) {
-            const uint32_t k = kg + 16 * i;
-            if (k >= nkeys) break;
-            float vf[8];
+        for (int r = 0; r < 4; ++r) {
+            const bool ok = kb + 4 * grp + r < nkeys && j < G;
+            pr[r] = ok ? __builtin_amdgcn_exp2f((s[r] - m_new) * LOG2E) : 0.f;
+        }
+        l_run = l_run * alpha + (pr[0] + pr[1] + pr[2] + pr[3]);
+        m_run = m_new;
+        // unconditional stores: no branch inside the loop body, which would let
+        // the compiler sink one block's FMAs past the next block's loads
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                vf[2 * e] = __uint_as_float(vr[i][e] << 16);
-                vf[2 * e + 1] = __uint_as_float(vr[i][e] & 0xffff0000u);
-            }
+        for (int r = 0; r < 4; ++r) xp[wave][4 * grp + r][j] = pr[r];
+        xa[wave][grp][j] = alpha;
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int h4 = 0; h4 < GT / 4; ++h4) {
+            const f32x4 al = *reinterpret_cast<const f32x4*>(&xa[wave][0][4 * h4]);
 #pragma unroll
             for (int hh = 0; hh < 4; ++hh) {
-                const float pr = (h0 + hh < G) ? sc[h0 + hh][k] : 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) o[hh][e] += pr * vf[e];
+                o[4 * h4 + hh][0] *= al[hh];
+                o[4 * h4 + hh][1] *= al[hh];
             }
         }
-        // lanes l, l^16, l^32, l^48 share dofs: fold the wave's four key groups
 #pragma unroll
-        for (int hh = 0; hh < 4; ++hh)
+        for (int i = 0; i < 16; ++i) {
+            const float v0 = __uint_as_float(blk.v[i] << 16);
+            const float v1 = __uint_as_float(blk.v[i] & 0xffff0000u);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                float v = o[hh][e];
-                v += __shfl_xor(v, 16);
-                v += __shfl_xor(v, 32);
-                o[hh][e] = v;
-            }
-        if (lane < 16) {
+            for (int h4 = 0; h4 < GT / 4; ++h4) {
+                const f32x4 ph = *reinterpret_cast<const f32x4*>(&xp[wave][i][4 * h4]);
 #pragma unroll
-            for (int hh = 0; hh < 4; ++hh)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) opart[wave][hh][dofs + e] = o[hh][e];
-        }
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t idx = tid + 256 * i, hh = idx / DH, d = idx % DH;
-            if (h0 + hh < G) {
-                const float v = opart[0][hh][d] + opart[1][hh][d] + opart[2][hh][d] +
-                                opart[3][hh][d];
-                st_sc1(ars, out_base + ((h0 + hh) * (DH + 2) + d) * 4, v);
+                for (int hh = 0; hh < 4; ++hh) {
+                    o[4 * h4 + hh][0] += ph[hh] * v0;
+                    o[4 * h4 + hh][1] += ph[hh] * v1;
+                }
             }
         }
-        __syncthreads();
-    }
-    if (tid < G) {
-        st_sc1(ars, out_base + (tid * (DH + 2) + DH) * 4, s_m[tid]);
-        st_sc1(ars, out_base + (tid * (DH + 2) + DH + 1) * 4, s_l[tid]);
-    }
-    if (!arrive_last(&p.attn_counters[bk], p.nchunks, &s_last)) return;
+        __builtin_amdgcn_wave_barrier();
+    };
 
-    // ---- merge the chunks of this (sequence, kv head): log-sum-exp rescaling ----
-    // Loads are batched eight chunks at a time so they are in flight together.
-    const uint32_t parts = bk * p.nchunks * G * (DH + 2) * 4;
-    constexpr uint32_t U = 8;
-    for (uint32_t idx = tid; idx < G * DH; idx += 256) {
-        const uint32_t h = idx / DH, d = idx % DH;
-        auto at = [&](uint32_t cc, uint32_t e) { return parts + ((cc * G + h) * (DH + 2) + e) * 4; };
-        float M = -INFINITY;
-        uint32_t cc = 0;
-        for (; cc + U <= p.nchunks; cc += U) {
-            float m[U];
+    // sched_barrier pins the order: a block's loads are issued right after the
+    // previous block's compute, so exactly two blocks are ever live.
+    for (uint32_t t = 0; t < nblk; t += 2) {
+        __builtin_amdgcn_sched_barrier(0);
+        load(bb, t + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(ba, t);
+        __builtin_amdgcn_sched_barrier(0);
+        load(ba, t + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(bb, t + 1);
+    }
+
+    // ---- fold each wave's key groups, then the four waves ----
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
 #pragma unroll
-            for (uint32_t u = 0; u < U; ++u) m[u] = ld_sc1(ars, at(cc + u, DH));
+    for (int h = 0; h < GT; ++h)
+        *reinterpret_cast<float2*>(&wo[wave][h][2 * lane]) = float2{o[h][0], o[h][1]};
+    if (grp == 0 && j < GT) { wm[wave][j] = m_run; wl[wave][j] = l_run; }
+    __syncthreads();
+
+    const __amdgpu_buffer_rsrc_t ars = coherent_rsrc(p.attn_part, p.attn_part_bytes);
+    const uint32_t part0 = (bk * p.nsplit + split) * G * APITCH * 4;
+    for (uint32_t idx = tid; idx < G * (DH / 4); idx += 256) {
+        const uint32_t h = idx / (DH / 4), d4 = idx % (DH / 4);
+        float M = NEG_BIG;
 #pragma unroll
-            for (uint32_t u = 0; u < U; ++u) M = fmaxf(M, m[u]);
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, wm[w][h]);
+        f32x4 O = {};
+        float L = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float sw = __builtin_amdgcn_exp2f((wm[w][h] - M) * LOG2E);
+            O += sw * *reinterpret_cast<const f32x4*>(&wo[w][h][4 * d4]);
+            L += sw * wl[w][h];
         }
-        for (; cc < p.nchunks; ++cc) M = fmaxf(M, ld_sc1(ars, at(cc, DH)));
-        float L = 0.f, O = 0.f;
-        for (cc = 0; cc + U <= p.nchunks; cc += U) {
-            float m[U], l[U], o[U];
+        st_sc1(ars, part0 + (h * APITCH + 4 * d4) * 4, O);
+        if (d4 == 0) {
+            st_sc1(ars, part0 + (h * APITCH + DH) * 4, M);
+            st_sc1(ars, part0 + (h * APITCH + DH + 1) * 4, L);
+        }
+    }
+    if (!arrive_last(&p.attn_counters[bk], p.nsplit, &s_last)) return;
+
+    // ---- merge: the splits' partials plus the new token ----
+    for (uint32_t h = wave; h < G; h += 4) {       // s_new = q . k_new (q is pre-scaled)
+        const uint32_t qa = *reinterpret_cast<const uint32_t*>(
+            p.q + (size_t)b * p.d + (kvh * G + h) * DH + 2 * lane);
+        const uint32_t ka = *reinterpret_cast<const uint32_t*>(knew + 2 * lane);
+        float d = __uint_as_float(qa << 16) * __uint_as_float(ka << 16) +
+                  __uint_as_float(qa & 0xffff0000u) * __uint_as_float(ka & 0xffff0000u);
+#pragma unroll
+        for (int o2 = 32; o2 > 0; o2 >>= 1) d += __shfl_xor(d, o2);
+        if (lane == 0) s_new[h] = d;
+    }
+    __syncthreads();
+    constexpr uint32_t U = 8;                      // splits per batch of loads
+    const uint32_t parts = bk * p.nsplit * G * APITCH * 4;
+    for (uint32_t idx = tid; idx < G * (DH / 4); idx += 256) {
+        const uint32_t h = idx / (DH / 4), d4 = idx % (DH / 4);
+        float M = NEG_BIG, L = 0.f;
+        f32x4 O = {};
+        for (uint32_t c0 = 0; c0 < p.nsplit; c0 += U) {
+            f32x4 oc[U];
+            float mc[U], lc[U];
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) {     // past the last split: reload it, weight 0
+                const uint32_t c = min(c0 + u, p.nsplit - 1);
+                const uint32_t at = parts + (c * G + h) * APITCH * 4;
+                oc[u] = ld4_sc1(ars, at + 16 * d4);
+                mc[u] = ld_sc1(ars, at + DH * 4);
+                lc[u] = ld_sc1(ars, at + (DH + 1) * 4);
+            }
+            float Mb = M;
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) Mb = fmaxf(Mb, mc[u]);
+            const float sc = __builtin_amdgcn_exp2f((M - Mb) * LOG2E);
+            O *= sc;
+            L *= sc;
 #pragma unroll
             for (uint32_t u = 0; u < U; ++u) {
-                m[u] = ld_sc1(ars, at(cc + u, DH));
-                l[u] = ld_sc1(ars, at(cc + u, DH + 1));
-                o[u] = ld_sc1(ars, at(cc + u, d));
+                const float w = c0 + u < p.nsplit ? __builtin_amdgcn_exp2f((mc[u] - Mb) * LOG2E) : 0.f;
+                O += w * oc[u];
+                L += w * lc[u];
             }
-#pragma unroll
-            for (uint32_t u = 0; u < U; ++u) {
-                const float w = expf(m[u] - M);
-                L += l[u] * w;
-                O += o[u] * w;
-            }
+            M = Mb;
         }
-        for (; cc < p.nchunks; ++cc) {
-            const float w = expf(ld_sc1(ars, at(cc, DH)) - M);
-            L += ld_sc1(ars, at(cc, DH + 1)) * w;
-            O += ld_sc1(ars, at(cc, d)) * w;
-        }
-        p.attn_out[(size_t)b * p.d + (kvh * G + h) * DH + d] = f2bf(O / L);
+        const float sn = s_new[h];
+        const float Mf = fmaxf(M, sn);
+        const float so = __builtin_amdgcn_exp2f((M - Mf) * LOG2E);
+        const float wn = __builtin_amdgcn_exp2f((sn - Mf) * LOG2E);
+        const uint2 vv = *reinterpret_cast<const uint2*>(vnew + 4 * d4);
+        const f32x4 vn = {__uint_as_float(vv.x << 16), __uint_as_float(vv.x & 0xffff0000u),
+                          __uint_as_float(vv.y << 16), __uint_as_float(vv.y & 0xffff0000u)};
+        const f32x4 res = (O * so + wn * vn) / (L * so + wn);
+        uint2 out;
+        out.x = (uint32_t)f2bf(res[0]) | ((uint32_t)f2bf(res[1]) << 16);
+        out.y = (uint32_t)f2bf(res[2]) | ((uint32_t)f2bf(res[3]) << 16);
+        *reinterpret_cast<uint2*>(p.attn_out + (size_t)b * p.d + (kvh * G + h) * DH + 4 * d4) = out;
     }
     reset_counter(&p.attn_counters[bk]);
 }
@@ -648,7 +702,7 @@ void attention_kernel(StepParams p) {
 // ---- host side -----------------------------------------------------------------------------
 
 struct Plan {
-    uint32_t nqkv, g, nchunks;
+    uint32_t nqkv, g, nsplit, split_keys;
     uint32_t tiles[4], splits[4];
     size_t off_counters, off_partial, off_sumsq, off_q, off_attn_part, off_attn_out, off_x1,
         off_x1b, off_x1b_lo, off_sumsq2, off_act, off_act_lo, total;
@@ -686,7 +740,17 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
     const uint32_t D = a->d_model, FF = a->d_ff, B = a->batch;
     pl->nqkv = D + 2 * a->n_kv_heads * DH;
     pl->g = a->n_heads / a->n_kv_heads;
-    pl->nchunks = a->cache_len == 0 ? 1u : (a->cache_len + LC - 1) / LC;
+    {   // attention: ~ATTN_WGS workgroups; splits of a multiple of 128 keys (an even
+        // number of 64-key iterations, as the loop is unrolled by two)
+        const uint32_t pairs = B * a->n_kv_heads;
+        const uint32_t want = std::max(1u, cdiv(ATTN_WGS, pairs));
+        const uint32_t nmax = std::max(1u, cdiv(a->cache_len, 2 * AKEYS));
+        const uint32_t per = cdiv(std::max(a->cache_len, 1u), std::min(want, nmax));
+        pl->split_keys = cdiv(per, 2 * AKEYS) * 2 * AKEYS;
+        pl->nsplit = std::max(1u, cdiv(a->cache_len, pl->split_keys));
+        if ((uint64_t)(pl->split_keys + 2 * AKEYS) * DH * 2 > 0xffffffffull)
+            return fail(MB_E_ARG, "decoder step: cache_len %u too large", a->cache_len);
+    }
     pl->tiles[EPI_QKV] = pl->nqkv / BN;
     pl->tiles[EPI_WO] = D / BN;
     pl->tiles[EPI_GU] = FF / 64;
@@ -711,7 +775,7 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
     pl->off_sumsq = o; o = align256(o + (size_t)pl->tiles[EPI_QKV] * pl->splits[EPI_QKV] * MROWS * 4);
     pl->off_q = o; o = align256(o + (size_t)B * D * 2);
     pl->off_attn_part = o;
-    o = align256(o + (size_t)B * a->n_kv_heads * pl->nchunks * pl->g * (DH + 2) * 4);
+    o = align256(o + (size_t)B * a->n_kv_heads * pl->nsplit * pl->g * APITCH * 4);
     pl->off_attn_out = o; o = align256(o + (size_t)B * D * 2);
     pl->off_x1 = o; o = align256(o + (size_t)B * D * 4);
     pl->off_x1b = o; o = align256(o + (size_t)B * D * 2);
@@ -749,8 +813,9 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
         return fail(MB_E_ARG, "decoder step: null pointer");
     const uintptr_t align_or = (uintptr_t)a->x | (uintptr_t)a->w_qkv | (uintptr_t)a->w_o |
                                (uintptr_t)a->w_gu | (uintptr_t)a->w_down |
-                               (uintptr_t)a->k_cache | (uintptr_t)a->v_cache;
-    if (align_or & 15) return fail(MB_E_ARG, "decoder step: inputs must be 16-byte aligned");
+                               (uintptr_t)a->k_cache | (uintptr_t)a->v_cache | (uintptr_t)a->y |
+                               (uintptr_t)a->k_new | (uintptr_t)a->v_new;
+    if (align_or & 15) return fail(MB_E_ARG, "decoder step: buffers must be 16-byte aligned");
 
     uint8_t* ws = static_cast<uint8_t*>(a->workspace);
     if (ws) {
@@ -765,7 +830,7 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
     StepParams p;
     p.batch = a->batch; p.d = a->d_model; p.hq = a->n_heads; p.hkv = a->n_kv_heads; p.g = pl.g;
     p.ff = a->d_ff; p.cache_len = a->cache_len; p.cache_stride = a->cache_stride;
-    p.nchunks = pl.nchunks; p.rope_base = a->rope_base; p.eps = a->eps;
+    p.nsplit = pl.nsplit; p.split_keys = pl.split_keys; p.rope_base = a->rope_base; p.eps = a->eps;
     p.x = a->x; p.k_cache = a->k_cache; p.v_cache = a->v_cache;
     p.y = a->y; p.k_new = a->k_new; p.v_new = a->v_new;
     uint32_t* counters = reinterpret_cast<uint32_t*>(ws + pl.off_counters);
@@ -809,8 +874,12 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
     launch_skinny<EPI_QKV>(g_qkv, p, s);
     MB_LAUNCH_CHECK("decoder qkv_rope");
     mark("attention");
-    hipLaunchKernelGGL(attention_kernel, dim3(a->batch * a->n_kv_heads * pl.nchunks), dim3(256),
-                       0, s, p);
+    {
+        const dim3 grid(a->batch * a->n_kv_heads * pl.nsplit), block(256);
+        if (pl.g <= 4) hipLaunchKernelGGL(attention_kernel<4>, grid, block, 0, s, p);
+        else if (pl.g <= 8) hipLaunchKernelGGL(attention_kernel<8>, grid, block, 0, s, p);
+        else hipLaunchKernelGGL(attention_kernel<16>, grid, block, 0, s, p);
+    }
     MB_LAUNCH_CHECK("decoder attention");
     mark("wo_residual");
     launch_skinny<EPI_WO>(g_wo, p, s);
