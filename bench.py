@@ -72,7 +72,7 @@ def _value_unit(name: str, meta: dict, ms_per_step: float):
     return meta["flops"] / (ms_per_step * 1e-3) / 1e12, "TFLOP/s", True
 
 
-def _roofline(w: dict, k_t: dict, compute_dtype: str) -> dict:
+def _roofline(name: str, w: dict, k_t: dict, compute_dtype: str) -> dict:
     if w["part"] is not None:
         part = next(p for p in k_t.get("parts", []) if p["name"] == w["part"])
         mean_ms = part["mean_ms"]
@@ -88,21 +88,23 @@ def _roofline(w: dict, k_t: dict, compute_dtype: str) -> dict:
         achieved = w["per_launch"] / sec / 1e12
         peak, unit = MFMA_PEAK_TFLOPS[compute_dtype], "TFLOP/s"
     out = {"bound": w["bound"], "achieved": achieved, "peak": peak, "unit": unit,
-           "frac": achieved / peak, "traffic": _traffic(kernel), "kernel_mean_us": mean_ms * 1e3}
+           "frac": achieved / peak, "traffic": _traffic(kernel or name),
+           "kernel_mean_us": mean_ms * 1e3}
     if kernel:
         out["kernel"] = kernel
     return out
 
 
-def _traffic(kernel) -> float | None:
-    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
-    summary (profiles/traffic.json), calibrated against a plain copy; None if
-    no counter run has been recorded for this kernel."""
+def _traffic(key: str) -> float | None:
+    """Bytes per launch that left the L2s (FETCH_SIZE x read scale + WRITE_SIZE
+    x write scale, both scales from a 256 MiB copy kernel) as recorded from
+    rocprofv3 --pmc runs in profiles/traffic.json, keyed by decoder part or
+    workload name; None if no counter run has been recorded for it."""
     p = REPO / "profiles" / "traffic.json"
     if not p.is_file():
         return None
     try:
-        return json.loads(p.read_text()).get(kernel or "", {}).get("bytes_per_launch")
+        return json.loads(p.read_text()).get(key, {}).get("bytes_per_launch")
     except Exception:
         return None
 
@@ -168,6 +170,27 @@ def _cpu_baseline(name: str, inputs, meta: dict) -> dict:
     return None
 
 
+def _copy_calibration(n_bytes: int = 256 << 20, launches: int = 3) -> None:
+    """Launch the plain copy kernel over a buffer of known size.  Under
+    `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE` its counter values are the
+    scale that turns the decoder kernels' counters into bytes."""
+    import torch
+
+    from metalbench_amd import native
+
+    n = n_bytes // 4
+    src = torch.randn(n, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    b = [native.make_binding(0, native.ROLE_INPUT, "f32", src.data_ptr(), n_bytes),
+         native.make_binding(1, native.ROLE_OUTPUT, "f32", dst.data_ptr(), n_bytes),
+         native.make_binding(2, native.ROLE_SCALAR, "u32", value=n)]
+    native.run(native.kernel_find("copy_f32"), b, 0, launches, native.RUN_PIPELINED)
+    torch.cuda.synchronize()
+    print(f"[bench] copy calibration: {launches} x copy_f32 of {n_bytes} bytes", file=sys.stderr,
+          flush=True)
+
+
 def _run_workload(name, steps, warmup, want_cpu):
     import torch
 
@@ -206,7 +229,7 @@ def _run_workload(name, steps, warmup, want_cpu):
     value, unit, hib = _value_unit(name, meta, ms_per_step)
     rec = {"value": value, "unit": unit, "higher_is_better": hib, "ms_per_step": ms_per_step,
            "gpu_median_ms": k_t["median_ms"], "gpu_mean_ms": k_t["mean_ms"],
-           "roofline": _roofline(w, k_t, b.compute_dtype), "dtype": b.compute_dtype}
+           "roofline": _roofline(name, w, k_t, b.compute_dtype), "dtype": b.compute_dtype}
     if k_t.get("parts"):
         rec["parts"] = [{"name": p["name"], "mean_us": p["mean_ms"] * 1e3,
                          **({"hbm_frac": w["parts"][p["name"]] / (p["mean_ms"] * 1e-3) / 1e9
@@ -227,6 +250,8 @@ def main(argv=None):
     ap.add_argument("--workload", default="llama_decoder_step")
     ap.add_argument("--only", action="store_true", help="skip the other configurations")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run the 256 MiB copy kernel (counter calibration)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -240,6 +265,8 @@ def main(argv=None):
     from metalbench_amd import native
     native.init(0)
     names = native.kernel_names()
+    if args.copy_calibration:
+        _copy_calibration()
 
     others = [n for n in ("transpose_2d", "sqr_mm", "conv2d", "large_mm") if n != args.workload]
     if args.only:

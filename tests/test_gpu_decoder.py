@@ -76,10 +76,10 @@ def _check(got, want, what):
     (2, 512, 4, 2, 1024, 40),      # smoke shape
     (1, 256, 2, 1, 384, 0),        # empty cache: attends to itself only
     (3, 512, 4, 4, 256, 5),        # MHA (G = 1)
-    (16, 1024, 8, 1, 512, 128),    # G = 8, exactly one full chunk + the new key
-    (5, 512, 4, 2, 640, 129),      # chunk boundary + 1
-    (7, 1024, 8, 2, 1024, 300),    # three chunks, ragged
-    (16, 2048, 16, 4, 1536, 1000),  # GQA 4 as the full config, many chunks
+    (16, 1024, 8, 1, 512, 128),    # G = 8, one full 128-key split + the new key
+    (5, 512, 4, 2, 640, 129),      # split boundary + 1
+    (7, 1024, 8, 2, 1024, 300),    # several 64-key blocks, ragged
+    (16, 2048, 16, 4, 1536, 1000),  # GQA 4 as the full config, several splits
 ])
 def test_decoder_step_shapes(mb, dev, B, D, H, HKV, FF, L):
     ins = _make(B, D, H, HKV, FF, L)
