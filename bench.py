@@ -10,11 +10,12 @@ configurations (sqr_mm, transpose_2d, conv2d, large_mm) are timed the same way
 and reported under "kernels", each with its own roofline fraction.
 
 Timing: W untimed steps, then exactly K steps launched back to back through
-mb_run (a hipEvent pair per step on the library stream), bracketed by
-torch.cuda.synchronize() on both sides; ms_per_step is the host wall clock of
-the K steps / K.  `roofline.achieved` is the algorithmic bytes (HBM-bound
+mb_run with no events in the stream, bracketed by torch.cuda.synchronize() on
+both sides; ms_per_step is the host wall clock of the K steps / K.  Then K more
+steps run with a hipEvent pair per step (and a mark before each kernel of a
+multi-kernel step): `roofline.achieved` is the algorithmic bytes (HBM-bound
 kernels) or flops (MFMA-bound kernels) of ONE launch of the dominant kernel
-divided by that kernel's mean event-timed duration over the same K steps.
+divided by that kernel's mean event-timed duration over those K steps.
 
 cpu_baseline: the float64 numpy oracle (oracle/), timed on this host on a
 bounded sample of the same workload — a reported baseline, not a target.
@@ -218,12 +219,18 @@ def _run_workload(name, steps, warmup, want_cpu):
     torch.cuda.synchronize()
     if warmup > 0:
         native.run(kid, bindings, 0, warmup, native.RUN_PIPELINED)
+    # Timed region: exactly `steps` launches back to back, no events in the
+    # stream, bracketed by synchronize on both sides.
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    k_t = native.run(kid, bindings, 0, steps, native.RUN_PIPELINED | native.RUN_PARTS)
+    native.run(kid, bindings, 0, steps, native.RUN_WALL_ONLY)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1000.0
     ms_per_step = wall_ms / steps
+    # Per-kernel durations (roofline): the same number of steps again, with a
+    # hipEvent pair per step and a mark before each kernel of the step.
+    k_t = native.run(kid, bindings, 0, steps, native.RUN_PIPELINED | native.RUN_PARTS)
+    torch.cuda.synchronize()
 
     w = _work(name, meta)
     value, unit, hib = _value_unit(name, meta, ms_per_step)

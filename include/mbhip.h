@@ -92,6 +92,8 @@ typedef struct mb_timing {
 #define MB_RUN_SYNC_EACH  0u  /* event pair + host sync per iteration (reference dispatchOnce) */
 #define MB_RUN_PIPELINED  1u  /* event pairs per iteration, one host sync at the end           */
 #define MB_RUN_PARTS      2u  /* also time each kernel of a multi-kernel entry                 */
+#define MB_RUN_WALL_ONLY  4u  /* no events: iters launches back to back, one host sync; every
+                                 statistic = host wall clock / iters (throughput timing)       */
 
 /* Device description; replaces detect_chip()/MChip (reference
  * metal/scripts/setup.h:26-46, setup.cpp:116-136). */

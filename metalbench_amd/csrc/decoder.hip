@@ -227,6 +227,29 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
             r[s][i] = *reinterpret_cast<const u32x4*>(wp + (size_t)(s * KS + i) * g.ldw);
     __builtin_amdgcn_sched_barrier(0);
 
+    // ---- epilogue inputs, in case this workgroup finishes the tile ----
+    // (issued behind the weights, so no weight wait grows; the finisher then
+    // needs one memory round trip, for the other splits' partials)
+    const uint32_t eb = tid >> 4, ec = 8 * (tid & 15);   // epilogue: row eb, columns ec .. ec+7
+    u32x4 pre_x = {};                                    // WO: x (bf16)
+    f32x4 pre_x1[2] = {f32x4{}, f32x4{}};                // DOWN: x1 (fp32)
+    float pre_ss[8] = {};                                // GU: sumsq2 terms, see finish_rows
+    if (EPI == EPI_WO)
+        pre_x = *reinterpret_cast<const u32x4*>(p.x + (size_t)(eb < p.batch ? eb : 0) * p.d +
+                                                tile * BN + ec);
+    if (EPI == EPI_DOWN) {
+        const float* src = p.x1 + (size_t)(eb < p.batch ? eb : 0) * p.d + tile * BN + ec;
+        pre_x1[0] = *reinterpret_cast<const f32x4*>(src);
+        pre_x1[1] = *reinterpret_cast<const f32x4*>(src + 4);
+    }
+    if (EPI == EPI_GU) {
+        const uint32_t ntile = p.d / BN;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            pre_ss[u] = p.sumsq2[min(eb + 16u * u, ntile - 1) * MROWS + (tid & 15)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
     // ---- activations -> LDS (they are the oldest loads) ----
 #pragma unroll
     for (int t = 0; t < NTERMS; ++t)
@@ -311,28 +334,24 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
     if (!arrive_last(&g.counters[tile], g.splits, &s_last)) return;
 
     // ---- finisher: this workgroup is the last of its tile ----
-    // float4 q of a tile = column q/4, rows 4*(q%4) .. +3; sum over the splits,
-    // eight splits (16 loads) in flight per lane.
+    // float4 q of a tile = column q/4, rows 4*(q%4) .. +3; sum over the splits
+    // with eight splits' loads in flight together (past the last split the
+    // last one is re-read and dropped, so no load sits behind a branch).
     {
-        constexpr uint32_t SPLIT_BYTES = MROWS * BN * 4;
+        constexpr uint32_t SPLIT_BYTES = MROWS * BN * 4, SB = 8;
         const uint32_t tile_base = tile * g.splits * SPLIT_BYTES;
         f32x4 v0 = {}, v1 = {};
-        uint32_t sp = 0;
-        for (; sp + 8 <= g.splits; sp += 8) {
-            f32x4 a[8], b[8];
+        for (uint32_t sp0 = 0; sp0 < g.splits; sp0 += SB) {
+            f32x4 a[SB], b[SB];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const uint32_t o = tile_base + (sp + u) * SPLIT_BYTES;
+            for (uint32_t u = 0; u < SB; ++u) {
+                const uint32_t o = tile_base + min(sp0 + u, g.splits - 1) * SPLIT_BYTES;
                 a[u] = ld4_sc1(prs, o + tid * 16);
                 b[u] = ld4_sc1(prs, o + (256 + tid) * 16);
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) { v0 += a[u]; v1 += b[u]; }
-        }
-        for (; sp < g.splits; ++sp) {
-            const uint32_t o = tile_base + sp * SPLIT_BYTES;
-            v0 += ld4_sc1(prs, o + tid * 16);
-            v1 += ld4_sc1(prs, o + (256 + tid) * 16);
+            for (uint32_t u = 0; u < SB; ++u)
+                if (sp0 + u < g.splits) { v0 += a[u]; v1 += b[u]; }
         }
         // red is row-major [16][BN] for the epilogues
 #pragma unroll
@@ -343,16 +362,40 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
             for (int e = 0; e < 4; ++e) red[(r0 + e) * BN + c] = v[e];
         }
     }
-    if (EPI == EPI_QKV && tid < MROWS) {
+    // Row statistics, thread (row = tid % 16, group = tid / 16) summing every
+    // 16th term, then the 16 groups through LDS:
+    //   QKV: sum of x^2 over the splits (sc1 loads, all in flight together);
+    //   GU:  sum of x1^2 over the W_o column tiles (prefetched) -> RMSNorm scale.
+    if (EPI == EPI_QKV || EPI == EPI_GU) {
+        float* scratch = red + MROWS * BN;   // 16 x 16 floats past the tile sums
+        const uint32_t row = tid & 15, grp = tid >> 4;
         float v = 0.f;
-        for (uint32_t sp = 0; sp < g.splits; ++sp)
-            v += ld_sc1(srs, ((tile * g.splits + sp) * MROWS + tid) * 4);
-        red_ss[tid] = v;
-    }
-    if (EPI == EPI_GU && tid < MROWS) {
-        float v = 0.f;
-        for (uint32_t t = 0; t < p.d / BN; ++t) v += p.sumsq2[t * MROWS + tid];
-        red_ss[tid] = rsqrtf(v / (float)p.d + p.eps);
+        if (EPI == EPI_QKV) {
+            constexpr uint32_t UT = 8;
+            for (uint32_t t0 = 0; t0 < g.splits; t0 += 16 * UT) {
+                float x[UT];
+#pragma unroll
+                for (uint32_t u = 0; u < UT; ++u) {
+                    const uint32_t t = min(t0 + grp + 16 * u, g.splits - 1);
+                    x[u] = ld_sc1(srs, ((tile * g.splits + t) * MROWS + row) * 4);
+                }
+#pragma unroll
+                for (uint32_t u = 0; u < UT; ++u)
+                    if (t0 + grp + 16 * u < g.splits) v += x[u];
+            }
+        } else {
+#pragma unroll
+            for (uint32_t u = 0; u < 8; ++u)
+                if (grp + 16 * u < p.d / BN) v += pre_ss[u];
+        }
+        scratch[grp * MROWS + row] = v;
+        __syncthreads();
+        if (tid < MROWS) {
+            float t = 0.f;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) t += scratch[q * MROWS + tid];
+            red_ss[tid] = EPI == EPI_QKV ? t : rsqrtf(t / (float)p.d + p.eps);
+        }
     }
     __syncthreads();
 
@@ -388,26 +431,34 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
             }
         }
     } else if (EPI == EPI_WO) {
+        // thread: row eb, columns ec .. ec+7; x1 = x + attn W_o
+        float v[8];
+        float sq = 0.f;
 #pragma unroll
-        for (int i = 0; i < (MROWS * BN) / 256; ++i) {
-            const uint32_t idx = tid + 256 * i, b = idx / BN, c = idx % BN;
-            float v = 0.f;
-            if (b < p.batch) {
-                const size_t o = (size_t)b * p.d + tile * BN + c;
-                v = bf2f(p.x[o]) + red[idx];
-                p.x1[o] = v;
-                const uint16_t hi = f2bf(v);
-                p.x1b[o] = hi;
-                p.x1b_lo[o] = f2bf(v - bf2f(hi));
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t xb = pre_x[e / 2] >> (16 * (e & 1));
+            v[e] = eb < p.batch ? bf2f((uint16_t)xb) + red[eb * BN + ec + e] : 0.f;
+            sq += v[e] * v[e];
+        }
+        if (eb < p.batch) {
+            const size_t o = (size_t)eb * p.d + tile * BN + ec;
+            *reinterpret_cast<f32x4*>(p.x1 + o) = f32x4{v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<f32x4*>(p.x1 + o + 4) = f32x4{v[4], v[5], v[6], v[7]};
+            u32x4 hi, lo;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint16_t h0 = f2bf(v[2 * e]), h1 = f2bf(v[2 * e + 1]);
+                hi[e] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                lo[e] = (uint32_t)f2bf(v[2 * e] - bf2f(h0)) |
+                        ((uint32_t)f2bf(v[2 * e + 1] - bf2f(h1)) << 16);
             }
-            red[idx] = v * v;
+            *reinterpret_cast<u32x4*>(p.x1b + o) = hi;
+            *reinterpret_cast<u32x4*>(p.x1b_lo + o) = lo;
         }
-        __syncthreads();
-        if (tid < MROWS) {
-            float v = 0.f;
-            for (int c = 0; c < BN; ++c) v += red[tid * BN + c];
-            p.sumsq2[tile * MROWS + tid] = v;
-        }
+        // row sums of x1^2 over the tile: the 16 threads of a row are 16 adjacent lanes
+#pragma unroll
+        for (int o2 = 8; o2 > 0; o2 >>= 1) sq += __shfl_xor(sq, o2);
+        if ((tid & 15) == 0) p.sumsq2[tile * MROWS + eb] = sq;
     } else if (EPI == EPI_GU) {
 #pragma unroll
         for (int i = 0; i < (MROWS * 64) / 256; ++i) {
@@ -421,13 +472,16 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
             p.act[o] = hi;
             p.act_lo[o] = f2bf(av - bf2f(hi));
         }
-    } else {   // EPI_DOWN
+    } else {   // EPI_DOWN: y = x1 + act W_down; thread: row eb, columns ec .. ec+7
+        if (eb < p.batch) {
+            u32x4 out;
 #pragma unroll
-        for (int i = 0; i < (MROWS * BN) / 256; ++i) {
-            const uint32_t idx = tid + 256 * i, b = idx / BN, c = idx % BN;
-            if (b >= p.batch) continue;
-            const size_t o = (size_t)b * p.d + tile * BN + c;
-            p.y[o] = f2bf(p.x1[o] + red[idx]);
+            for (int e = 0; e < 4; ++e) {
+                const float y0 = pre_x1[e / 2][2 * (e & 1)] + red[eb * BN + ec + 2 * e];
+                const float y1 = pre_x1[e / 2][2 * (e & 1) + 1] + red[eb * BN + ec + 2 * e + 1];
+                out[e] = (uint32_t)f2bf(y0) | ((uint32_t)f2bf(y1) << 16);
+            }
+            *reinterpret_cast<u32x4*>(p.y + (size_t)eb * p.d + tile * BN + ec) = out;
         }
     }
     reset_counter(&g.counters[tile]);   // ready for the next step
@@ -729,6 +783,8 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
         return fail(MB_E_ARG, "decoder step: more than %d query heads per kv head", MAXG);
     if ((uint64_t)a->n_heads * DH != a->d_model)
         return fail(MB_E_ARG, "decoder step: d_model %u != n_heads * head_dim", a->d_model);
+    if (a->d_model > 16384)   // the RMSNorm scale reads at most 8 x 16 column-tile sums per row
+        return fail(MB_E_ARG, "decoder step: d_model %u > 16384", a->d_model);
     if (a->d_ff == 0 || a->d_ff % KS)
         return fail(MB_E_ARG, "decoder step: d_ff %u must be a positive multiple of %d", a->d_ff,
                     KS);

@@ -320,6 +320,22 @@ int mb_run(int id, const mb_binding* bindings, int n_bindings, int warmup, int i
     }
     MB_HIP_TRY(hipStreamSynchronize(s));
 
+    if (flags & MB_RUN_WALL_ONLY) {   // no events: launches back to back, one sync
+        auto w0 = std::chrono::steady_clock::now();
+        for (int it = 0; it < iters; ++it) {
+            int rc = k.launch(bs, s, nullptr);
+            if (rc) return rc;
+        }
+        hipError_t r = hipStreamSynchronize(s);
+        if (r != hipSuccess) return fail(MB_E_HIP, "kernel execution failed: %s", hipGetErrorString(r));
+        const double wall = std::chrono::duration<double, std::milli>(
+                                std::chrono::steady_clock::now() - w0).count();
+        memset(out, 0, sizeof(*out));
+        out->iters = iters;
+        out->wall_ms = wall;
+        out->min_ms = out->median_ms = out->mean_ms = wall / iters;
+        return MB_OK;
+    }
     const bool pipelined = flags & MB_RUN_PIPELINED;
     const bool parts = (flags & MB_RUN_PARTS) && k.n_parts > 1;
     const int np = parts ? std::min(k.n_parts, MB_MAX_PARTS) : 0;

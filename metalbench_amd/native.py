@@ -31,6 +31,7 @@ DTYPE_CODE = {"f32": 0, "f16": 1, "i32": 2, "u32": 3, "bf16": 4}
 RUN_SYNC_EACH = 0
 RUN_PIPELINED = 1
 RUN_PARTS = 2
+RUN_WALL_ONLY = 4
 MAX_PARTS = 8
 
 
