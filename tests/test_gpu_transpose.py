@@ -12,7 +12,8 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("rows,cols", [
     (1, 1), (1, 7), (7, 1), (64, 64), (63, 65), (65, 63), (128, 192), (1000, 3),
-    (3, 1000), (333, 777), (1024, 2048), (2048, 1024), (4096, 64),
+    (3, 1000), (333, 777), (1024, 2048), (2048, 1024), (4096, 64), (128, 128), (256, 384),
+    (258, 386), (130, 4096),
 ])
 def test_transpose_bit_exact(mb, dev, rows, cols):
     a = seeded(rows * 7919 + cols, (rows, cols))
@@ -33,12 +34,26 @@ def test_transpose_specials_bit_exact(mb, dev):
     # NaN payloads, infinities, signed zeros and denormals move unchanged.
     vals = np.array([np.nan, -np.nan, np.inf, -np.inf, 0.0, -0.0, 1e-45, -1e-40, 3.0],
                     np.float32)
-    a = np.resize(vals, (96, 80)).astype(np.float32)
+    # 256 x 160: full 128 x 128 tiles (vector path) and an edge strip.
+    a = np.resize(vals, (256, 160)).astype(np.float32)
     a.view(np.uint32)[5, 7] = 0x7FA00001            # signalling-NaN payload
+    a.view(np.uint32)[200, 140] = 0xFFC00123
     d_a = torch.from_numpy(a).to(dev)
-    d_b = torch.zeros((80, 96), device=dev)
-    launch("mb_launch_transpose_2d_f32", ptr(d_a), ptr(d_b), 96, 80, None)
+    d_b = torch.zeros((160, 256), device=dev)
+    launch("mb_launch_transpose_2d_f32", ptr(d_a), ptr(d_b), 256, 160, None)
     assert np.array_equal(bits32(d_b), oracle.transpose(a).view(np.int32))
+
+
+def test_transpose_unaligned_pointers_take_the_scalar_path(mb, dev):
+    # A and B one float past a 16-byte boundary: full tiles, but no float4 access.
+    rows, cols = 256, 384
+    a = seeded(11, (rows, cols))
+    buf_a = torch.zeros(rows * cols + 4, device=dev)
+    buf_b = torch.full((rows * cols + 4,), float("nan"), device=dev)
+    buf_a[1:1 + rows * cols] = a.reshape(-1).to(dev)
+    launch("mb_launch_transpose_2d_f32", ptr(buf_a) + 4, ptr(buf_b) + 4, rows, cols, None)
+    got = buf_b[1:1 + rows * cols].cpu().numpy().view(np.int32).reshape(cols, rows)
+    assert np.array_equal(got, oracle.transpose(a.numpy()).view(np.int32))
 
 
 @pytest.mark.parametrize("name", ["transpose_2d", "transpose_2d_ref"])
