@@ -213,6 +213,214 @@ void gemm_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
         }
 }
 
+// ---- full-tile kernel (M, N multiples of 256, K of 128, operands < 2 GiB) ----
+// A goes to LDS by DMA (buffer_load ... lds): no registers, no LDS store
+// instructions.  The DMA writes each wave's 64 lanes x 16 B contiguously, so
+// A rows are stored unpadded (128 B = 8 chunks of 8 k) with chunk c of row r
+// in slot c ^ ((r / 2) % 8): lane l of a DMA fetches the chunk its slot will
+// hold, and the MFMA operand reads stay conflict free (a ds_read_b128 serves
+// 16 lanes = 16 consecutive rows per LDS cycle; their 16-byte bank groups
+// 8 (r % 2) + slot are then all distinct).
+// B keeps the register path (8 x 16-byte rows per lane, v_perm_b32 transpose,
+// ds_write into the pitch-72 layout) with TWO register stages in flight, so a
+// B load has two LDS stages (~2 x 64 MFMAs per wave) to arrive; the VGPRs for
+// the second stage are the ones A no longer needs.
+// Stage s: DMA A(s+1) -> As[(s+1)%2], load B(s+2) -> rb[s%2], MFMAs on
+// As/Bs[s%2], store B(s+1) from rb[(s+1)%2] -> Bs[(s+1)%2], wait for the DMA,
+// barrier.  Every buffer is its own __shared__ array and the loop is unrolled
+// by two, so the compiler tracks each DMA target separately and never waits
+// for the B loads still in flight.
+constexpr int ROWB = BK * 2;              // bytes per unpadded A row in LDS
+
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__global__ __launch_bounds__(256, 1)
+void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+                           uint16_t* __restrict__ C, uint32_t M, uint32_t N, uint32_t K,
+                           uint32_t tiles_m, uint32_t tiles_n) {
+    __shared__ __attribute__((aligned(1024))) uint16_t As0[BM * BK];
+    __shared__ __attribute__((aligned(1024))) uint16_t As1[BM * BK];
+    __shared__ __attribute__((aligned(16))) uint16_t Bs0[TILE_ELEMS];
+    __shared__ __attribute__((aligned(16))) uint16_t Bs1[TILE_ELEMS];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: DMA bases
+    const uint32_t wm = wave >> 1, wn = wave & 1;
+    uint32_t tm, tn;
+    tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(tm * BM);
+    const uint32_t n0 = __builtin_amdgcn_readfirstlane(tn * BN);
+    const uint32_t nstages = K / BK;
+    const uint32_t last_k0 = (nstages - 1) * BK;
+
+    const __amdgpu_buffer_rsrc_t ars =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A), 0, M * K * 2, 0x00020000u);
+    const __amdgpu_buffer_rsrc_t brs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(B), 0, K * N * 2, 0x00020000u);
+
+    // A DMA: instruction i of wave w fills rows R = 64 w + 8 i + l/8, slot l%8,
+    // which holds chunk (l%8) ^ ((R/2) % 8) = (l%8) ^ ((4 (i%2) + l/16) % 8).
+    const uint32_t a_r = lane >> 3;
+    const uint32_t a_voff0 = ((64 * wave + a_r) * K + 8 * ((lane & 7) ^ (a_r >> 1))) * 2;
+    const uint32_t a_voff1 = ((64 * wave + a_r) * K + 8 * ((lane & 7) ^ ((4 + (a_r >> 1)) & 7))) * 2;
+    auto dma_a = [&](uint16_t* dst, uint32_t k0, int i0, int i1) {   // instructions [i0, i1)
+#pragma unroll
+        for (int i = i0; i < i1; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ars, (__attribute__((address_space(3))) void*)(dst + (64 * wave + 8 * i) * BK), 16,
+                (i & 1) ? a_voff1 : a_voff0, ((m0 + 8 * i) * K + k0) * 2, 0, 0);
+    };
+    // B: k-octet ko = tid%8, n-octet no = tid/8 (8 rows of 16 B each).
+    const uint32_t b_ko = tid & 7, b_no = tid >> 3;
+    const uint32_t b_voff = (8 * b_ko * N + 8 * b_no) * 2;
+    u32x4 rb[2][8];
+    auto load_b = [&](int st, uint32_t k0, int r0, int r1) {   // rows [r0, r1)
+#pragma unroll
+        for (int r = r0; r < r1; ++r)
+            rb[st][r] = __builtin_amdgcn_raw_buffer_load_b128(brs, b_voff, ((k0 + r) * N + n0) * 2, 0);
+    };
+    auto store_b = [&](int st, uint16_t* bs) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            uint32_t lo[4], hi[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                lo[j] = __builtin_amdgcn_perm(rb[st][2 * j + 1][m], rb[st][2 * j][m], 0x05040100u);
+                hi[j] = __builtin_amdgcn_perm(rb[st][2 * j + 1][m], rb[st][2 * j][m], 0x07060302u);
+            }
+            *reinterpret_cast<u32x4*>(bs + (8 * b_no + 2 * m) * PITCH + 8 * b_ko) =
+                u32x4{lo[0], lo[1], lo[2], lo[3]};
+            *reinterpret_cast<u32x4*>(bs + (8 * b_no + 2 * m + 1) * PITCH + 8 * b_ko) =
+                u32x4{hi[0], hi[1], hi[2], hi[3]};
+        }
+    };
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+    const uint32_t li = lane & 31, lh = lane >> 5;
+    // One LDS stage of MFMAs.  The next stages' global loads are spread over
+    // the four k steps (`pre(kk)` issues a quarter: 4 loads per 16 MFMAs, so
+    // the texture unit never backs up into the wave's in-order issue), and
+    // `post` (the B transpose + LDS stores of the next stage) runs inside k
+    // step 3; one instruction group per MFMA, so nothing but the initial
+    // operand reads sits outside the MFMA shadow.
+    auto mfma_stage = [&](const uint16_t* as_base, const uint16_t* bs_base, auto&& pre,
+                          auto&& post) {
+        const uint8_t* as = reinterpret_cast<const uint8_t*>(as_base) + (wm * 128 + li) * ROWB;
+        const uint16_t* bs = bs_base + (wn * 128 + li) * PITCH + 8 * lh;
+        auto a_at = [&](int i, int kk) {   // rows wm*128 + 32 i + li, k chunk 2 kk + lh, swizzled
+            return *reinterpret_cast<const bf16x8*>(as + 32 * i * ROWB +
+                                                    16 * ((2 * kk + lh) ^ ((li >> 1) & 7)));
+        };
+        bf16x8 a[2][4], b[2][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[0][i] = a_at(i, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[0][j] = *reinterpret_cast<const bf16x8*>(bs + 32 * j * PITCH);
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; ++kk) {
+            const int c = kk & 1;
+            __builtin_amdgcn_sched_barrier(0);
+            pre(kk);
+            if (kk + 1 < BK / 16) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) a[c ^ 1][i] = a_at(i, kk + 1);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    b[c ^ 1][j] = *reinterpret_cast<const bf16x8*>(bs + 32 * j * PITCH + 16 * (kk + 1));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[c][i], b[c][j], acc[i][j],
+                                                                         0, 0, 0);
+            if (kk == BK / 16 - 1) post();
+            if (kk + 1 < BK / 16) {   // 16 MFMA, 8 operand reads, 4 global loads
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
+                }
+            } else {                  // 16 MFMA, 4 global loads, 32 v_perm + 8 LDS stores
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
+                    __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // DS write
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
+                    __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // DS write
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // every DMA of this thread done (the 8 B loads issued after them may not be)
+    auto wait_dma = [] { __builtin_amdgcn_s_waitcnt(0xF78); };   // vmcnt(8) expcnt(7) lgkmcnt(15)
+
+    dma_a(As0, 0, 0, 8);
+    load_b(0, 0, 0, 8);
+    __builtin_amdgcn_s_waitcnt(0);
+    store_b(0, Bs0);
+    __syncthreads();
+    load_b(1, min((uint32_t)BK, last_k0), 0, 8);
+    // nstages is even (K % 128 == 0), so the body is straight-line: past the
+    // last stage the clamped loads re-read it and the stores write buffers
+    // that are never read again.
+    // k steps 0, 1: A DMA of the next stage (4 + 4); k steps 2, 3: B loads of
+    // the stage after (4 + 4)
+    for (uint32_t s = 0; s < nstages; s += 2) {
+        const uint32_t ka = (s + 1) * BK, kb = min((s + 2) * BK, last_k0);
+        mfma_stage(As0, Bs0,
+                   [&](int kk) {
+                       if (kk < 2) dma_a(As1, ka, 4 * kk, 4 * kk + 4);
+                       else load_b(0, kb, 4 * (kk - 2), 4 * (kk - 2) + 4);
+                   },
+                   [&] { store_b(1, Bs1); });
+        wait_dma();
+        lds_barrier();
+        const uint32_t ka2 = min((s + 2) * BK, last_k0), kb2 = min((s + 3) * BK, last_k0);
+        mfma_stage(As1, Bs1,
+                   [&](int kk) {
+                       if (kk < 2) dma_a(As0, ka2, 4 * kk, 4 * kk + 4);
+                       else load_b(1, kb2, 4 * (kk - 2), 4 * (kk - 2) + 4);
+                   },
+                   [&] { store_b(0, Bs0); });
+        wait_dma();
+        lds_barrier();
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // no DMA may still target LDS at the end
+
+    // Epilogue: lane l, reg r of a 32x32 block -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t gc = n0 + wn * 128 + 32 * j + li;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t gr = m0 + wm * 128 + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
+                C[(size_t)gr * N + gc] = f32_to_bf16_rne(acc[i][j][r]);
+            }
+        }
+}
+
 constexpr size_t SMEM_BYTES = 4 * TILE_ELEMS * sizeof(uint16_t);   // 147456
 
 int launch_gemm_bf16(const uint16_t* a, const uint16_t* b, uint16_t* c, uint32_t m, uint32_t n,
@@ -224,7 +432,8 @@ int launch_gemm_bf16(const uint16_t* a, const uint16_t* b, uint16_t* c, uint32_t
     if (nblocks > 0x7fffffffull) return fail(MB_E_ARG, "matmul_bf16: shape too large");
     const bool aligned = (k % 8 == 0) && (n % 8 == 0) &&
                          ((((uintptr_t)a) | ((uintptr_t)b)) & 15) == 0;
-    const bool full = aligned && m % BM == 0 && n % BN == 0 && k % BK == 0;
+    const bool full = aligned && m % BM == 0 && n % BN == 0 && k % (2 * BK) == 0 && k > 0 &&
+                      (uint64_t)m * k * 2 < (1ull << 31) && (uint64_t)k * n * 2 < (1ull << 31);
     static bool attr_set[3] = {false, false, false};
     auto go = [&](auto kernel, int mode) -> int {
         if (!attr_set[mode]) {
@@ -238,7 +447,12 @@ int launch_gemm_bf16(const uint16_t* a, const uint16_t* b, uint16_t* c, uint32_t
         MB_LAUNCH_CHECK("matmul_bf16");
         return MB_OK;
     };
-    if (full) return go(gemm_bf16_kernel<MODE_FULL>, MODE_FULL);
+    if (full) {
+        hipLaunchKernelGGL(gemm_bf16_full_kernel, dim3((uint32_t)nblocks), dim3(256), 0, s, a, b, c,
+                           m, n, k, tiles_m, tiles_n);
+        MB_LAUNCH_CHECK("matmul_bf16");
+        return MB_OK;
+    }
     if (aligned) return go(gemm_bf16_kernel<MODE_GUARD>, MODE_GUARD);
     return go(gemm_bf16_kernel<MODE_ELEM>, MODE_ELEM);
 }
@@ -261,7 +475,7 @@ int run_gemm_bf16(const Bindings& bs, hipStream_t s, PartMarks*) {
 
 void register_gemm_bf16() {
     register_kernel({"large_matmul_bf16", run_gemm_bf16,
-                     reinterpret_cast<const void*>(&gemm_bf16_kernel<MODE_FULL>), 1});
+                     reinterpret_cast<const void*>(&gemm_bf16_full_kernel), 1});
 }
 
 }  // namespace mb
