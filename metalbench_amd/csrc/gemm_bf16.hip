@@ -263,17 +263,23 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
     const __amdgpu_buffer_rsrc_t brs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(B), 0, K * N * 2, 0x00020000u);
 
-    // A DMA: instruction i of wave w fills rows R = 64 w + 8 i + l/8, slot l%8,
-    // which holds chunk (l%8) ^ ((R/2) % 8) = (l%8) ^ ((4 (i%2) + l/16) % 8).
-    const uint32_t a_r = lane >> 3;
-    const uint32_t a_voff0 = ((64 * wave + a_r) * K + 8 * ((lane & 7) ^ (a_r >> 1))) * 2;
-    const uint32_t a_voff1 = ((64 * wave + a_r) * K + 8 * ((lane & 7) ^ ((4 + (a_r >> 1)) & 7))) * 2;
-    auto dma_a = [&](uint16_t* dst, uint32_t k0, int i0, int i1) {   // instructions [i0, i1)
+    // A: lane loads rows a_row + 32 i (i < 8), 16-byte chunk a_chunk, and
+    // stores them into the swizzled layout (slot = chunk ^ ((row / 2) % 8)).
+    const uint32_t a_row = tid >> 3, a_chunk = tid & 7;
+    const uint32_t a_voff = (a_row * K + 8 * a_chunk) * 2;
+    u32x4 ra[2][8];
+    auto load_a = [&](int st, uint32_t k0, int i0, int i1) {
 #pragma unroll
         for (int i = i0; i < i1; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                ars, (__attribute__((address_space(3))) void*)(dst + (64 * wave + 8 * i) * BK), 16,
-                (i & 1) ? a_voff1 : a_voff0, ((m0 + 8 * i) * K + k0) * 2, 0, 0);
+            ra[st][i] = __builtin_amdgcn_raw_buffer_load_b128(ars, a_voff, ((m0 + 32 * i) * K + k0) * 2, 0);
+    };
+    auto store_a = [&](int st, uint16_t* as_dst) {
+        uint8_t* as = reinterpret_cast<uint8_t*>(as_dst);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t row = a_row + 32 * i;
+            *reinterpret_cast<u32x4*>(as + row * ROWB + 16 * (a_chunk ^ ((row >> 1) & 7))) = ra[st][i];
+        }
     };
     // B: k-octet ko = tid%8, n-octet no = tid/8 (8 rows of 16 B each).
     const uint32_t b_ko = tid & 7, b_no = tid >> 3;
@@ -355,57 +361,56 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
                     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
                 }
-            } else {                  // 16 MFMA, 4 global loads, 32 v_perm + 8 LDS stores
+            } else {                  // 16 MFMA, 4 global loads, 32 v_perm + 16 LDS stores
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
                     __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read
+                    __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);   // DS write
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
                     __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
                     __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // DS write
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
                     __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
                     __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // DS write
-                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
                 }
             }
         }
         __builtin_amdgcn_sched_barrier(0);
     };
-    // every DMA of this thread done (the 8 B loads issued after them may not be)
-    auto wait_dma = [] { __builtin_amdgcn_s_waitcnt(0xF78); };   // vmcnt(8) expcnt(7) lgkmcnt(15)
 
-    dma_a(As0, 0, 0, 8);
+    load_a(0, 0, 0, 8);
     load_b(0, 0, 0, 8);
     __builtin_amdgcn_s_waitcnt(0);
+    store_a(0, As0);
     store_b(0, Bs0);
     __syncthreads();
+    load_a(1, min((uint32_t)BK, last_k0), 0, 8);
     load_b(1, min((uint32_t)BK, last_k0), 0, 8);
-    // nstages is even (K % 128 == 0), so the body is straight-line: past the
-    // last stage the clamped loads re-read it and the stores write buffers
-    // that are never read again.
-    // k steps 0, 1: A DMA of the next stage (4 + 4); k steps 2, 3: B loads of
-    // the stage after (4 + 4)
+    // Stage s: MFMAs on buffers s % 2; register set s % 2 receives stage s+2
+    // (A in k steps 0-1, B in 2-3); set (s+1) % 2, loaded one stage earlier,
+    // is stored to the other buffers inside k step 3.  nstages is even
+    // (K % 128 == 0), so the body is straight-line: past the last stage the
+    // clamped loads re-read it and land in buffers never read again.
     for (uint32_t s = 0; s < nstages; s += 2) {
-        const uint32_t ka = (s + 1) * BK, kb = min((s + 2) * BK, last_k0);
+        const uint32_t k2 = min((s + 2) * BK, last_k0), k3 = min((s + 3) * BK, last_k0);
         mfma_stage(As0, Bs0,
                    [&](int kk) {
-                       if (kk < 2) dma_a(As1, ka, 4 * kk, 4 * kk + 4);
-                       else load_b(0, kb, 4 * (kk - 2), 4 * (kk - 2) + 4);
+                       if (kk < 2) load_a(0, k2, 4 * kk, 4 * kk + 4);
+                       else load_b(0, k2, 4 * (kk - 2), 4 * (kk - 2) + 4);
                    },
-                   [&] { store_b(1, Bs1); });
-        wait_dma();
+                   [&] { store_a(1, As1); store_b(1, Bs1); });
         lds_barrier();
-        const uint32_t ka2 = min((s + 2) * BK, last_k0), kb2 = min((s + 3) * BK, last_k0);
         mfma_stage(As1, Bs1,
                    [&](int kk) {
-                       if (kk < 2) dma_a(As0, ka2, 4 * kk, 4 * kk + 4);
-                       else load_b(1, kb2, 4 * (kk - 2), 4 * (kk - 2) + 4);
+                       if (kk < 2) load_a(1, k3, 4 * kk, 4 * kk + 4);
+                       else load_b(1, k3, 4 * (kk - 2), 4 * (kk - 2) + 4);
                    },
-                   [&] { store_b(0, Bs0); });
-        wait_dma();
+                   [&] { store_a(0, As0); store_b(0, Bs0); });
         lds_barrier();
     }
-    __builtin_amdgcn_s_waitcnt(0);   // no DMA may still target LDS at the end
+
 
     // Epilogue: lane l, reg r of a 32x32 block -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
 #pragma unroll
