@@ -412,18 +412,32 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
     }
 
 
-    // Epilogue: lane l, reg r of a 32x32 block -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
+    // Epilogue through LDS: each wave converts its 128 x 128 tile to bf16
+    // (hardware round-to-nearest-even convert), writes it row-major into its
+    // own 32 KB of the now idle operand buffers, and streams it out as 16-byte
+    // row chunks (a wave store instruction covers four 256-byte row segments).
+    // Lane l, reg r of 32x32 block (i, j): row 32 i + 8 (r/4) + 4 (l/32) + r%4,
+    // column 32 j + l%32.
+    lds_barrier();   // every wave is done reading the operand buffers
+    uint16_t* ct = wave == 0 ? As0 : wave == 1 ? As1 : wave == 2 ? Bs0 : Bs1;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t gc = n0 + wn * 128 + 32 * j + li;
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const uint32_t gr = m0 + wm * 128 + 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
-                C[(size_t)gr * N + gc] = f32_to_bf16_rne(acc[i][j][r]);
+                const uint32_t row = 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
+                ct[row * 128 + 32 * j + li] = __builtin_bit_cast(uint16_t, (__bf16)acc[i][j][r]);
             }
-        }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+#pragma unroll
+    for (int q = 0; q < 32; ++q) {
+        const uint32_t row = 4 * q + (lane >> 4), ch = lane & 15;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(ct + row * 128 + 8 * ch);
+        *reinterpret_cast<u32x4*>(C + (size_t)(m0 + wm * 128 + row) * N + n0 + wn * 128 + 8 * ch) = v;
+    }
 }
 
 constexpr size_t SMEM_BYTES = 4 * TILE_ELEMS * sizeof(uint16_t);   // 147456
