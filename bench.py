@@ -9,9 +9,14 @@ decoder decode step ("decoder block us/step"); the other four
 configurations (sqr_mm, transpose_2d, conv2d, large_mm) are timed the same way
 and reported under "kernels", each with its own roofline fraction.
 
-Timing: W untimed steps, then exactly K steps launched back to back through
-mb_run with no events in the stream, bracketed by torch.cuda.synchronize() on
-both sides; ms_per_step is the host wall clock of the K steps / K.  Then K more
+Timing: W untimed steps, then exactly K steps launched back to back with no
+events in the stream, bracketed by torch.cuda.synchronize() on both sides;
+ms_per_step is the host wall clock of the K steps / K.  The HBM-bound
+workloads (decoder step, transpose) are timed cold: each step uses the next of
+R device copies of its working set (R x 570 MB for the decoder, R x 536 MB for
+the transpose), through the typed C entry point, so the 256 MB memory-side
+cache cannot serve one step from the previous one; the others reuse one set
+of buffers through mb_run.  Then K more
 steps run with a hipEvent pair per step (and a mark before each kernel of a
 multi-kernel step): `roofline.achieved` is the algorithmic bytes (HBM-bound
 kernels) or flops (MFMA-bound kernels) of ONE launch of the dominant kernel
@@ -192,6 +197,60 @@ def _copy_calibration(n_bytes: int = 256 << 20, launches: int = 3) -> None:
           flush=True)
 
 
+# HBM-bound workloads are timed cold: their working set (weights + KV cache,
+# or the matrix being transposed) is rotated over R device copies, so no step
+# finds the previous step's bytes in the 256 MB memory-side cache (MALL) -- as
+# in a real decode, where every layer streams its own weights and cache.
+ROTATE = {"llama_decoder_step": 3, "transpose_2d": 2}
+
+
+def _async_launcher(name, b, copies_in, copies_out):
+    """Per-copy launch through the typed C entry point (asynchronous, library
+    stream), for the rotating timed loop; None for non-rotating workloads."""
+    import ctypes
+
+    from metalbench_amd import native
+
+    lib = native.load()
+    sc = {s.binding: s.value for s in b.scalars()}
+    if name == "llama_decoder_step":
+        args = []
+        for ci, co in zip(copies_in, copies_out):
+            a = native.MbDecoderStepArgs()
+            a.batch, a.d_model, a.n_heads, a.n_kv_heads = sc[10], sc[11], sc[12], sc[13]
+            a.head_dim, a.d_ff, a.cache_len, a.cache_stride = 128, sc[14], sc[15], sc[15]
+            a.rope_base, a.eps = sc[16], sc[17]
+            (a.x, a.w_qkv, a.w_o, a.w_gu, a.w_down, a.k_cache, a.v_cache) = [t.data_ptr() for t in ci]
+            a.y, a.k_new, a.v_new = [t.data_ptr() for t in co]
+            a.workspace, a.workspace_bytes = None, 0
+            args.append(a)
+
+        def launch(c):
+            native.check("mb_launch_llama_decoder_step_bf16",
+                         lib.mb_launch_llama_decoder_step_bf16(ctypes.byref(args[c]), None))
+        return launch
+    if name == "transpose_2d":
+        rows, cols = sc[2], sc[3]
+
+        def launch(c):
+            native.check("mb_launch_transpose_2d_f32", lib.mb_launch_transpose_2d_f32(
+                copies_in[c][0].data_ptr(), copies_out[c][0].data_ptr(), rows, cols, None))
+        return launch
+    return None
+
+
+def _mean_timing(runs: list) -> dict:
+    """Average single-iteration mb_run timings (and their per-kernel parts)."""
+    out = {"mean_ms": sum(r["mean_ms"] for r in runs) / len(runs)}
+    ms = sorted(r["mean_ms"] for r in runs)
+    out["median_ms"] = ms[len(ms) // 2]
+    if runs[0].get("parts"):
+        out["parts"] = [{"name": p["name"],
+                         "mean_ms": sum(r["parts"][i]["mean_ms"] for r in runs) / len(runs)}
+                        for i, p in enumerate(runs[0]["parts"])]
+    return out
+
+
 def _run_workload(name, steps, warmup, want_cpu):
     import torch
 
@@ -202,47 +261,72 @@ def _run_workload(name, steps, warmup, want_cpu):
     meta = b.meta
     inputs = b.make_inputs(0)
     dev = torch.device("cuda", 0)
-    d_in = [t.to(dev) for t in inputs]
-    d_out = [torch.zeros(tuple(o.shape), dtype=H.torch_dtype(o.dtype), device=dev)
-             for o in b.outputs]
-    bindings = []
-    for binding, t, dt in zip(b.input_bindings, d_in, b.input_dtypes):
-        bindings.append(native.make_binding(binding, native.ROLE_INPUT, dt, t.data_ptr(),
-                                            t.numel() * t.element_size()))
-    for o, t in zip(b.outputs, d_out):
-        bindings.append(native.make_binding(o.binding, native.ROLE_OUTPUT, o.dtype,
-                                            t.data_ptr(), t.numel() * t.element_size()))
-    for s in b.scalars():
-        bindings.append(native.make_binding(s.binding, native.ROLE_SCALAR, s.dtype,
-                                            value=s.value))
+    R = ROTATE.get(name, 1)
+    copies_in = [[t.to(dev) for t in inputs]]
+    copies_out = [[torch.zeros(tuple(o.shape), dtype=H.torch_dtype(o.dtype), device=dev)
+                   for o in b.outputs]]
+    for _ in range(R - 1):
+        copies_in.append([t.clone() for t in copies_in[0]])
+        copies_out.append([t.clone() for t in copies_out[0]])
+
+    def bindings_for(ci, co):
+        bs = []
+        for binding, t, dt in zip(b.input_bindings, ci, b.input_dtypes):
+            bs.append(native.make_binding(binding, native.ROLE_INPUT, dt, t.data_ptr(),
+                                          t.numel() * t.element_size()))
+        for o, t in zip(b.outputs, co):
+            bs.append(native.make_binding(o.binding, native.ROLE_OUTPUT, o.dtype, t.data_ptr(),
+                                          t.numel() * t.element_size()))
+        for s in b.scalars():
+            bs.append(native.make_binding(s.binding, native.ROLE_SCALAR, s.dtype, value=s.value))
+        return bs
+
+    bind_sets = [bindings_for(ci, co) for ci, co in zip(copies_in, copies_out)]
     kid = native.kernel_find(b.metal_function)
+    launch = _async_launcher(name, b, copies_in, copies_out) if R > 1 else None
     torch.cuda.synchronize()
     if warmup > 0:
-        native.run(kid, bindings, 0, warmup, native.RUN_PIPELINED)
+        if launch:
+            for i in range(warmup):
+                launch(i % R)
+        else:
+            native.run(kid, bind_sets[0], 0, warmup, native.RUN_PIPELINED)
     # Timed region: exactly `steps` launches back to back, no events in the
     # stream, bracketed by synchronize on both sides.
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    native.run(kid, bindings, 0, steps, native.RUN_WALL_ONLY)
+    if launch:
+        for i in range(steps):
+            launch(i % R)
+    else:
+        native.run(kid, bind_sets[0], 0, steps, native.RUN_WALL_ONLY)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1000.0
     ms_per_step = wall_ms / steps
-    # Per-kernel durations (roofline): the same number of steps again, with a
-    # hipEvent pair per step and a mark before each kernel of the step.
-    k_t = native.run(kid, bindings, 0, steps, native.RUN_PIPELINED | native.RUN_PARTS)
+    # Per-kernel durations (roofline): `steps` more steps with a hipEvent pair
+    # per step and a mark before each kernel of the step; rotating workloads
+    # run them one by one over the copies, so each is timed cold as well.
+    if R > 1:
+        k_t = _mean_timing([native.run(kid, bind_sets[i % R], 0, 1,
+                                       native.RUN_PIPELINED | native.RUN_PARTS)
+                            for i in range(steps)])
+    else:
+        k_t = native.run(kid, bind_sets[0], 0, steps, native.RUN_PIPELINED | native.RUN_PARTS)
     torch.cuda.synchronize()
 
     w = _work(name, meta)
     value, unit, hib = _value_unit(name, meta, ms_per_step)
     rec = {"value": value, "unit": unit, "higher_is_better": hib, "ms_per_step": ms_per_step,
            "gpu_median_ms": k_t["median_ms"], "gpu_mean_ms": k_t["mean_ms"],
-           "roofline": _roofline(name, w, k_t, b.compute_dtype), "dtype": b.compute_dtype}
+           "roofline": _roofline(name, w, k_t, b.compute_dtype), "dtype": b.compute_dtype,
+           "cache": (f"cold: {R} rotating copies of the working set" if R > 1
+                     else "warm: one set of buffers")}
     if k_t.get("parts"):
         rec["parts"] = [{"name": p["name"], "mean_us": p["mean_ms"] * 1e3,
                          **({"hbm_frac": w["parts"][p["name"]] / (p["mean_ms"] * 1e-3) / 1e9
                              / HBM_PEAK_GBPS} if "parts" in w and p["name"] in w["parts"] else {})}
                         for p in k_t["parts"]]
-    del d_in, d_out
+    del copies_in, copies_out
     torch.cuda.synchronize()
     if want_cpu:
         rec["cpu_baseline"] = _cpu_baseline(name, inputs, meta)
@@ -314,6 +398,7 @@ def main(argv=None):
         "data": "synthetic (seed 0; registry input_init distributions)",
         "config": config,
         "roofline": head["roofline"],
+        "cache": head["cache"],
         "cpu_baseline": head.get("cpu_baseline"),
         "gpu_mean_ms": head["gpu_mean_ms"],
         "parts": head.get("parts"),
