@@ -89,6 +89,7 @@ __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 //   reader: the workgroup that brought the counter to its final value reads
 //           every partial with sc1 loads.
 constexpr int CPOL_SC1 = 16;                  // cache policy: sc1 (device coherent)
+constexpr int CPOL_NT = 2;                    // cache policy: nt (streamed, read once per step)
 constexpr uint32_t RSRC_FLAGS = 0x00020000u;  // buffer descriptor word 3: 32-bit data format
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base, uint32_t bytes) {
@@ -224,7 +225,8 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
     for (int s = 0; s < NSTEPS; ++s)
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-            r[s][i] = *reinterpret_cast<const u32x4*>(wp + (size_t)(s * KS + i) * g.ldw);
+            r[s][i] = __builtin_nontemporal_load(   // streamed once per step
+                reinterpret_cast<const u32x4*>(wp + (size_t)(s * KS + i) * g.ldw));
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- epilogue inputs, in case this workgroup finishes the tile ----
@@ -569,10 +571,10 @@ void attention_kernel(StepParams p) {
         const uint32_t base = t * AKEYS * DH * 2;
 #pragma unroll
         for (int m = 0; m < 4; ++m)
-            blk.k[m] = __builtin_amdgcn_raw_buffer_load_b128(krs, base + koff + 64 * m, 0, 0);
+            blk.k[m] = __builtin_amdgcn_raw_buffer_load_b128(krs, base + koff + 64 * m, 0, CPOL_NT);
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-            blk.v[i] = __builtin_amdgcn_raw_buffer_load_b32(vrs, base + voff + i * DH * 2, 0, 0);
+            blk.v[i] = __builtin_amdgcn_raw_buffer_load_b32(vrs, base + voff + i * DH * 2, 0, CPOL_NT);
     };
 
     // q rows of the G heads go to LDS (the MFMA B operand is re-read per
