@@ -17,8 +17,9 @@
 //                     free), RoPE, writes q (bf16, pre-scaled by 1/sqrt(Dh))
 //                     and k_new / v_new (bf16);
 //   2. attention      flash-decoding: one workgroup per (sequence, kv head,
-//                     64-key chunk); q.k^T on MFMA, softmax, p.v on VALU; the
-//                     last chunk to finish merges the chunks (log-sum-exp);
+//                     split of the cached keys); q.k^T on MFMA, online
+//                     softmax, p.v on VALU; the last split to finish merges
+//                     the splits and the new token (log-sum-exp);
 //   3. wo_residual    skinny GEMM attn @ W_o, finisher adds x, writes x1
 //                     (fp32 + bf16) and per-tile sums of x1^2;
 //   4. gate_up_swiglu skinny GEMM x1 @ [W_gate | W_up], each tile holding 64
@@ -39,7 +40,9 @@
 // LDS (pitch 136 bf16, chunk index XOR-swizzled by (row / 16) so both the
 // stores and the ds_read_b128 operand reads are bank-conflict free).  The
 // activations are the MFMA A operand (16 rows = the batch, zero-filled above
-// it), read straight from L2.  v_mfma_f32_16x16x32_bf16 accumulates; split-K
+// it), parked in LDS before the weights arrive.  Weights are loaded
+// non-temporal (each byte is read once per step).
+// v_mfma_f32_16x16x32_bf16 accumulates; split-K
 // partials go to the workspace and the LAST workgroup of each column tile (an
 // atomic counter, reset by that workgroup) sums them and runs the epilogue;
 // the partials travel through device-coherent (sc1) accesses, not fences.

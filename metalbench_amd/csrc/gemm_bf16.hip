@@ -11,7 +11,9 @@
 //    128x128 sub-tile = 4x4 v_mfma_f32_32x32x16_bf16 accumulators (256 fp32
 //    per lane, held in AccVGPRs); one workgroup per CU, 1024 tiles at 8192^3 =
 //    exactly four rounds of 256 CUs;
-//  * LDS double buffer: both operands stored K-contiguous, row pitch 72 bf16
+//  * (the guarded / element-wise kernel; the full-tile kernel further down
+//    keeps the tile shape but swizzles A and stages loads two ahead)
+//    LDS double buffer: both operands stored K-contiguous, row pitch 72 bf16
 //    (144 B), 2 x 2 x 36 KB = 144 KB of the 160 KB.  With that pitch the MFMA
 //    operand reads (ds_read_b128 of 16 consecutive rows) and both store
 //    patterns below touch distinct bank groups;
@@ -214,22 +216,25 @@ void gemm_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
 }
 
 // ---- full-tile kernel (M, N multiples of 256, K of 128, operands < 2 GiB) ----
-// A goes to LDS by DMA (buffer_load ... lds): no registers, no LDS store
-// instructions.  The DMA writes each wave's 64 lanes x 16 B contiguously, so
-// A rows are stored unpadded (128 B = 8 chunks of 8 k) with chunk c of row r
-// in slot c ^ ((r / 2) % 8): lane l of a DMA fetches the chunk its slot will
-// hold, and the MFMA operand reads stay conflict free (a ds_read_b128 serves
-// 16 lanes = 16 consecutive rows per LDS cycle; their 16-byte bank groups
-// 8 (r % 2) + slot are then all distinct).
-// B keeps the register path (8 x 16-byte rows per lane, v_perm_b32 transpose,
-// ds_write into the pitch-72 layout) with TWO register stages in flight, so a
-// B load has two LDS stages (~2 x 64 MFMAs per wave) to arrive; the VGPRs for
-// the second stage are the ones A no longer needs.
-// Stage s: DMA A(s+1) -> As[(s+1)%2], load B(s+2) -> rb[s%2], MFMAs on
-// As/Bs[s%2], store B(s+1) from rb[(s+1)%2] -> Bs[(s+1)%2], wait for the DMA,
-// barrier.  Every buffer is its own __shared__ array and the loop is unrolled
-// by two, so the compiler tracks each DMA target separately and never waits
-// for the B loads still in flight.
+// Both operands are register-staged TWO LDS stages ahead: the global loads
+// for stage s+2 are issued during the MFMAs of stage s, so a load has about
+// 2 x 64 MFMAs per wave (~4 us at the power-limited clock) to arrive.
+//  * A rows are stored unpadded (128 B = 8 chunks of 8 k) with chunk c of row
+//    r in slot c ^ ((r / 2) % 8): a ds_read_b128 serves 16 lanes = 16
+//    consecutive rows per LDS cycle, and their 16-byte bank groups
+//    8 (r % 2) + slot are then all distinct (conflict free);
+//  * B (N-contiguous in HBM) is loaded as 8 x 16-byte rows per lane,
+//    transposed in registers with v_perm_b32 and stored K-contiguous into
+//    the pitch-72 layout;
+//  * stage s: loads of stage s+2 -> register set s % 2 (A in k steps 0-1, B
+//    in k steps 2-3, 4 loads per 16 MFMAs), MFMAs on LDS buffers s % 2, and
+//    in k step 3 the stores of register set (s+1) % 2 into buffers
+//    (s+1) % 2; then an LDS-only barrier (lgkmcnt + s_barrier, the global
+//    loads stay in flight).  sched_group_barrier interleaves one MFMA with
+//    each group of loads / operand reads / transposes / stores, so the MFMA
+//    pipe never waits on issue.
+// Buffer-to-LDS DMA for A (no registers, no LDS store instructions) was
+// measured slower than this on MI355X (49% vs 50.6% of peak at 8192^3).
 constexpr int ROWB = BK * 2;              // bytes per unpadded A row in LDS
 
 __device__ __forceinline__ void lds_barrier() {
