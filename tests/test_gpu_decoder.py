@@ -75,15 +75,28 @@ def _check(got, want, what):
 @pytest.mark.parametrize("B,D,H,HKV,FF,L", [
     (2, 512, 4, 2, 1024, 40),      # smoke shape
     (1, 256, 2, 1, 384, 0),        # empty cache: attends to itself only
+    (2, 512, 4, 2, 512, 0),        # empty cache, 512-row K splits
     (3, 512, 4, 4, 256, 5),        # MHA (G = 1)
+    (4, 512, 4, 4, 512, 5),        # MHA (G = 1), 512-row K splits
     (16, 1024, 8, 1, 512, 128),    # G = 8, one full 128-key split + the new key
     (5, 512, 4, 2, 640, 129),      # split boundary + 1
     (7, 1024, 8, 2, 1024, 300),    # several 64-key blocks, ragged
     (16, 2048, 16, 4, 1536, 1000),  # GQA 4 as the full config, several splits
+    (9, 2048, 16, 1, 1024, 77),    # G = 16
 ])
 def test_decoder_step_shapes(mb, dev, B, D, H, HKV, FF, L):
     ins = _make(B, D, H, HKV, FF, L)
     _check(_run(dev, ins, B, D, H, HKV, FF, L), _want(ins, H, HKV, L), f"{B,D,H,HKV,FF,L}")
+
+
+def test_decoder_step_new_inputs_every_call(mb, dev):
+    """Back-to-back steps on different data through one workspace: no call may
+    see an earlier call's intermediates (queries, attention, x1, SwiGLU)."""
+    cfg = (16, 1024, 8, 2, 1024, 256)
+    B, D, H, HKV, FF, L = cfg
+    for seed in (21, 22, 23):
+        ins = _make(*cfg, seed=seed)
+        _check(_run(dev, ins, *cfg), _want(ins, H, HKV, L), f"seed {seed}")
 
 
 def test_decoder_step_padded_stride_and_caller_workspace(mb, dev):
