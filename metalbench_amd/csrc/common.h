@@ -65,6 +65,8 @@ struct Bindings {
                void** ptr, const char* what) const;
     int u32(uint32_t idx, uint32_t* v, const char* what) const;
     int f32(uint32_t idx, float* v, const char* what) const;
+    // Byte size of buffer binding `idx` (0 if it is missing or not a buffer).
+    uint64_t nbytes(uint32_t idx) const;
 };
 
 // One registry entry: the `metal_function` name and its launcher.
@@ -83,7 +85,36 @@ void register_gemm_f32();
 void register_conv2d();
 void register_gemm_bf16();
 void register_decoder();
+void register_transformer_f32();
 
 static inline uint32_t cdiv(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
+
+// ---- fp32 GEMM family (gemm_f32.hip), shared with the transformer kernels ----
+// C[b] = A[b] @ B[b] (row-major, leading dimensions lda/ldb/ldc), batch b at
+// blockIdx.y with element strides batch_*.  Kinds:
+//   PLAIN       C = A B
+//   RMS         C = rmsnorm(A) B            (row scale rsqrt(mean(A_row^2) + eps), K = row length)
+//   RMS_BT      C = rmsnorm(A) B^T, B [N][K]
+//   RESID       C = A B + R                 (R [M][N], leading dimension ldr)
+//   SWIGLU      C = silu(A B) * (A B2)
+//   RMS_SWIGLU  C = silu(rmsnorm(A) B) * (rmsnorm(A) B2)
+struct GemmF32Args {
+    const float* a;
+    const float* b;
+    const float* b2;
+    float* c;
+    const float* r;
+    uint32_t m, n, k, lda, ldb, ldc, ldr, tiles_n;
+    uint64_t batch_a, batch_b, batch_c;
+    float eps;
+};
+enum GemmF32Kind {
+    GEMM_F32_PLAIN, GEMM_F32_RMS, GEMM_F32_RMS_BT, GEMM_F32_RESID, GEMM_F32_SWIGLU,
+    GEMM_F32_RMS_SWIGLU
+};
+// Dense row-major defaults: lda = k, ldb = ldc = ldr = n, no batch stride.
+GemmF32Args gemm_f32_args(const float* a, const float* b, float* c, uint32_t m, uint32_t n,
+                          uint32_t k);
+int launch_gemm_f32_ex(GemmF32Args g, GemmF32Kind kind, uint32_t batch, hipStream_t s);
 
 }  // namespace mb

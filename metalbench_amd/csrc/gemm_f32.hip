@@ -1,10 +1,21 @@
-// fp32 GEMM C[M][N] = A[M][K] @ B[K][N] (row-major), on fp32 MFMA.
-//
-// Spec: reference mlx/kernels/common/sqr_mm.py:10-11 (mx.matmul), registry
-// mlx/kernels/common/registry.py:43-59 and :129 (A@0, B@1, C@2, M@3, N@4,
-// K@5; 2*M*N*K flops, 4*(MK+KN+MN) bytes).  The reference kernel reads only N
-// (metal/kernels/common/sqr_mm.metal:23); this one honours M, N and K and any
-// shape, including ragged edges.
+// fp32 GEMM family on fp32 MFMA: C[M][N] = A[M][K] @ B (row-major), with
+// optional batching, a transposed B, an RMSNorm row scale and fused
+// epilogues.  One kernel template serves these registry entries:
+//   sqr_mm, rect_mm, fused_qkv_projection   plain C = A B
+//     (reference mlx/kernels/common/sqr_mm.py:10-11, rect_mm.py:10-11,
+//      standard/fused_qkv_projection.py:12-13; registry common/registry.py:
+//      43-59,129-130, standard/registry.py:324-337: A@0 B@1 C@2 M@3 N@4 K@5)
+//   batch_mm                                C[b] = A[b] B[b]
+//     (common/batch_mm.py:10-11, registry common/registry.py:61-77,131)
+//   rms_norm_linear                         C = rmsnorm(A) W^T, W [N][K]
+//     (standard/rms_norm_linear.py:12-14, registry standard/registry.py:26-42)
+//   swiglu                                  C = silu(A Wg) * (A Wu)
+//     (standard/swiglu.py:9-10, registry standard/registry.py:119-133)
+// and the prefill decoder layer's GEMMs (RMSNorm row scale, residual add,
+// SwiGLU over the [gate | up] halves of one weight).
+// The reference kernel reads only N (metal/kernels/common/sqr_mm.metal:23);
+// these honour M, N, K, leading dimensions and any shape, including ragged
+// edges.
 //
 // gfx950 design.  fp32 MFMA peak is 256 flop/clk/CU (157.3 TFLOP/s), so at
 // 1024^3 the whole problem is ~32k MFMA cycles per CU: the kernel must keep one
@@ -17,10 +28,15 @@
 //    partial accumulators are summed through LDS at the end;
 //  * A is staged K-contiguous (As[m][k], row stride 36 floats: 16 lanes reading
 //    16 consecutive rows with ds_read_b128 cover all 64 banks once);
-//    B is staged N-contiguous (Bs[k][n], row stride 68 floats);
+//    B [K][N] is staged N-contiguous (Bs[k][n], row stride 68 floats); a
+//    transposed B ([N][K]) is staged like A and read like A;
 //  * K order inside a stage is permuted consistently for A and B: lane l holds
 //    A[i][8g + 4*(l/32) + t] for MFMA t of group g and reads the matching row
-//    of Bs, so one ds_read_b128 feeds four MFMAs.  The sum over k is the same.
+//    of Bs, so one ds_read_b128 feeds four MFMAs.  The sum over k is the same;
+//  * RMSNorm row scale: rmsnorm(x) W = diag(r) (x W), r = rsqrt(mean(x^2) +
+//    eps), and the sum of squares comes from the A loads the tile makes
+//    anyway (every thread of the workgroup loads A, whichever K half it
+//    multiplies), so the normalised rows are never materialised.
 #include "common.h"
 
 namespace mb {
@@ -29,18 +45,25 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 64, BN = 64, BK = 32;
-constexpr int SA = BK + 4;   // As row stride (floats)
+constexpr int SA = BK + 4;   // As (and transposed Bs) row stride (floats)
 constexpr int SB = BN + 4;   // Bs row stride (floats)
 
-template <int KSPLIT, bool VEC>
+enum { BL_KN = 0, BL_NK = 1 };                           // B is [K][N] or [N][K]
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2 };   // C = acc | acc + R | silu(acc) acc2
+
+__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
+
+template <int KSPLIT, bool VEC, int BL, int EPI, bool RMS>
 __global__ __launch_bounds__(256 * KSPLIT)
-void gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B,
-                     float* __restrict__ C, uint32_t M, uint32_t N, uint32_t K,
-                     uint32_t tiles_n) {
+void gemm_f32_kernel(GemmF32Args g) {
     constexpr int NT = 256 * KSPLIT;
     constexpr int LOADS = 512 / NT;   // float4 per thread per operand per stage
+    constexpr bool DUAL = EPI == EPI_SWIGLU;
+    constexpr int NB = DUAL ? 2 : 1;
+    constexpr int BSZ = BL == BL_KN ? BK * SB : BN * SA;
     __shared__ __attribute__((aligned(16))) float As[2][BM * SA];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BK * SB];
+    __shared__ __attribute__((aligned(16))) float Bs[2][NB][BSZ];
+    __shared__ float rscale[BM];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63;
@@ -48,48 +71,45 @@ void gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B,
     const uint32_t wk = wave >> 2;            // K half (KSPLIT == 2)
     const uint32_t wm = (wave >> 1) & 1;
     const uint32_t wn = wave & 1;
-    const uint32_t tm = blockIdx.x / tiles_n;
-    const uint32_t tn = blockIdx.x - tm * tiles_n;
+    const uint32_t tm = blockIdx.x / g.tiles_n;
+    const uint32_t tn = blockIdx.x - tm * g.tiles_n;
     const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t M = g.m, N = g.n, K = g.k;
     const uint32_t nstages = (K + BK - 1) / BK;
+    const float* A = g.a + (size_t)blockIdx.y * g.batch_a;
+    const float* Bp[2] = {g.b + (size_t)blockIdx.y * g.batch_b,
+                          DUAL ? g.b2 + (size_t)blockIdx.y * g.batch_b : nullptr};
+    float* C = g.c + (size_t)blockIdx.y * g.batch_c;
 
-    float4 ra[LOADS], rb[LOADS];
+    float4 ra[LOADS], rb[NB][LOADS];
+    float ss[LOADS] = {};   // RMS: this thread's sum of squares of its A row
 
+    auto load4 = [&](const float* base, uint32_t ld, uint32_t row, uint32_t rows, uint32_t col,
+                     uint32_t cols) -> float4 {
+        if (VEC)
+            return (row < rows && col < cols)
+                       ? *reinterpret_cast<const float4*>(base + (size_t)row * ld + col)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            v[e] = (row < rows && col + e < cols) ? base[(size_t)row * ld + col + e] : 0.f;
+        return make_float4(v[0], v[1], v[2], v[3]);
+    };
     auto load = [&](uint32_t k0) {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             const uint32_t q = tid + i * NT;
             // A: 64 rows x 8 float4
-            {
-                const uint32_t row = q >> 3, kq = (q & 7) * 4;
-                const uint32_t gm = m0 + row, gk = k0 + kq;
-                if (VEC) {
-                    ra[i] = (gm < M && gk < K)
-                                ? *reinterpret_cast<const float4*>(A + (size_t)gm * K + gk)
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
-                } else {
-                    float v[4];
+            ra[i] = load4(A, g.lda, m0 + (q >> 3), M, k0 + (q & 7) * 4, K);
+            if (RMS) ss[i] += ra[i].x * ra[i].x + ra[i].y * ra[i].y + ra[i].z * ra[i].z +
+                              ra[i].w * ra[i].w;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        v[e] = (gm < M && gk + e < K) ? A[(size_t)gm * K + gk + e] : 0.f;
-                    ra[i] = make_float4(v[0], v[1], v[2], v[3]);
-                }
-            }
-            // B: 32 rows x 16 float4
-            {
-                const uint32_t krow = q >> 4, nq = (q & 15) * 4;
-                const uint32_t gk = k0 + krow, gn = n0 + nq;
-                if (VEC) {
-                    rb[i] = (gk < K && gn < N)
-                                ? *reinterpret_cast<const float4*>(B + (size_t)gk * N + gn)
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
-                } else {
-                    float v[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        v[e] = (gk < K && gn + e < N) ? B[(size_t)gk * N + gn + e] : 0.f;
-                    rb[i] = make_float4(v[0], v[1], v[2], v[3]);
-                }
+            for (int o = 0; o < NB; ++o) {
+                if (BL == BL_KN)   // B: 32 rows (k) x 16 float4 (n)
+                    rb[o][i] = load4(Bp[o], g.ldb, k0 + (q >> 4), K, n0 + (q & 15) * 4, N);
+                else               // B^T: 64 rows (n) x 8 float4 (k), like A
+                    rb[o][i] = load4(Bp[o], g.ldb, n0 + (q >> 3), N, k0 + (q & 7) * 4, K);
             }
         }
     };
@@ -98,11 +118,19 @@ void gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B,
         for (int i = 0; i < LOADS; ++i) {
             const uint32_t q = tid + i * NT;
             *reinterpret_cast<float4*>(&As[buf][(q >> 3) * SA + (q & 7) * 4]) = ra[i];
-            *reinterpret_cast<float4*>(&Bs[buf][(q >> 4) * SB + (q & 15) * 4]) = rb[i];
+#pragma unroll
+            for (int o = 0; o < NB; ++o) {
+                if (BL == BL_KN)
+                    *reinterpret_cast<float4*>(&Bs[buf][o][(q >> 4) * SB + (q & 15) * 4]) = rb[o][i];
+                else
+                    *reinterpret_cast<float4*>(&Bs[buf][o][(q >> 3) * SA + (q & 7) * 4]) = rb[o][i];
+            }
         }
     };
 
-    f32x16 acc = {};
+    f32x16 acc[NB];
+#pragma unroll
+    for (int o = 0; o < NB; ++o) acc[o] = f32x16{};
     const uint32_t li = lane & 31;     // row (A) / column (B) inside the 32x32 sub-tile
     const uint32_t lh = lane >> 5;     // which 4-wide K quarter of a group
 
@@ -115,67 +143,134 @@ void gemm_f32_kernel(const float* __restrict__ A, const float* __restrict__ B,
         const int cur = s & 1;
         if (s + 1 < nstages) load((s + 1) * BK);
         const float* as = &As[cur][(wm * 32 + li) * SA + 4 * lh];
-        const float* bs = &Bs[cur][(4 * lh) * SB + wn * 32 + li];
 #pragma unroll
         for (int gg = 0; gg < 4 / KSPLIT; ++gg) {
-            const int g = (int)wk * (4 / KSPLIT) + gg;
-            const float4 a4 = *reinterpret_cast<const float4*>(as + 8 * g);
-            const float b0 = bs[(8 * g + 0) * SB];
-            const float b1 = bs[(8 * g + 1) * SB];
-            const float b2 = bs[(8 * g + 2) * SB];
-            const float b3 = bs[(8 * g + 3) * SB];
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.x, b0, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.y, b1, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.z, b2, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.w, b3, acc, 0, 0, 0);
+            const int gi = (int)wk * (4 / KSPLIT) + gg;
+            const float4 a4 = *reinterpret_cast<const float4*>(as + 8 * gi);
+#pragma unroll
+            for (int o = 0; o < NB; ++o) {
+                float4 b4;
+                if (BL == BL_KN) {
+                    const float* bs = &Bs[cur][o][(4 * lh) * SB + wn * 32 + li];
+                    b4 = make_float4(bs[(8 * gi + 0) * SB], bs[(8 * gi + 1) * SB],
+                                     bs[(8 * gi + 2) * SB], bs[(8 * gi + 3) * SB]);
+                } else {
+                    b4 = *reinterpret_cast<const float4*>(
+                        &Bs[cur][o][(wn * 32 + li) * SA + 4 * lh + 8 * gi]);
+                }
+                acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.x, b4.x, acc[o], 0, 0, 0);
+                acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.y, b4.y, acc[o], 0, 0, 0);
+                acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.z, b4.z, acc[o], 0, 0, 0);
+                acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.w, b4.w, acc[o], 0, 0, 0);
+            }
         }
         if (s + 1 < nstages) store(cur ^ 1);
         __syncthreads();
     }
 
+    if (RMS) {   // the 8 threads of an A row are 8 adjacent lanes (q & 7)
+        static_assert(LOADS == 1, "one A row per thread");
+        float t = ss[0];
+        t += __shfl_xor(t, 1);
+        t += __shfl_xor(t, 2);
+        t += __shfl_xor(t, 4);
+        if ((tid & 7) == 0 && tid < 8 * BM) rscale[tid >> 3] = rsqrtf(t / (float)K + g.eps);
+    }
+
     if (KSPLIT == 2) {
         // Second K half hands its partial sums to the first through LDS
-        // (4 waves x 64 lanes x 16 floats = 16 KB, inside As).
+        // (4 waves x 64 lanes x 16 floats = 16 KB, inside As), one operand at a time.
         float* red = &As[0][0];
-        if (wk == 1) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) red[((wave & 3) * 16 + r) * 64 + lane] = acc[r];
+        for (int o = 0; o < NB; ++o) {
+            if (wk == 1) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) red[((wave & 3) * 16 + r) * 64 + lane] = acc[o][r];
+            }
+            __syncthreads();
+            if (wk == 0) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[o][r] += red[((wave & 3) * 16 + r) * 64 + lane];
+            }
+            __syncthreads();
         }
-        __syncthreads();
         if (wk == 1) return;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] += red[((wave & 3) * 16 + r) * 64 + lane];
+    } else if (RMS) {
+        __syncthreads();
     }
 
     // 32x32 accumulator layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
     const uint32_t gc = n0 + wn * 32 + li;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-        const uint32_t gr = m0 + wm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        if (gr < M && gc < N) C[(size_t)gr * N + gc] = acc[r];
+        const uint32_t lr = wm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        const uint32_t gr = m0 + lr;
+        if (gr < M && gc < N) {
+            const float sc = RMS ? rscale[lr] : 1.0f;
+            float v;
+            if (EPI == EPI_SWIGLU) v = silu_f(acc[0][r] * sc) * (acc[NB - 1][r] * sc);
+            else if (EPI == EPI_RESID) v = acc[0][r] * sc + g.r[(size_t)gr * g.ldr + gc];
+            else v = acc[0][r] * sc;
+            C[(size_t)gr * g.ldc + gc] = v;
+        }
     }
 }
 
-int launch_gemm_f32(const float* a, const float* b, float* c, uint32_t m, uint32_t n,
-                    uint32_t k, hipStream_t s) {
-    if (m == 0 || n == 0) return MB_OK;
-    if (!a || !b || !c) return fail(MB_E_ARG, "matmul_f32: null pointer");
-    const uint32_t tiles_m = cdiv(m, BM), tiles_n = cdiv(n, BN);
-    const uint64_t nblocks = (uint64_t)tiles_m * tiles_n;
-    if (nblocks > 0x7fffffffull) return fail(MB_E_ARG, "matmul_f32: shape too large");
-    const bool vec = (k % 4 == 0) && (n % 4 == 0) &&
-                     (((uintptr_t)a | (uintptr_t)b) & 15) == 0;
-    if (vec)
-        hipLaunchKernelGGL((gemm_f32_kernel<2, true>), dim3((uint32_t)nblocks), dim3(512), 0, s,
-                           a, b, c, m, n, k, tiles_n);
-    else
-        hipLaunchKernelGGL((gemm_f32_kernel<2, false>), dim3((uint32_t)nblocks), dim3(512), 0, s,
-                           a, b, c, m, n, k, tiles_n);
+template <int BL, int EPI, bool RMS>
+int launch_variant(const GemmF32Args& g, uint32_t batch, hipStream_t s) {
+    const uint64_t nblocks = (uint64_t)cdiv(g.m, BM) * g.tiles_n;
+    if (nblocks > 0x7fffffffull || batch > 65535)
+        return fail(MB_E_ARG, "matmul_f32: shape too large");
+    // float4 paths need 16-byte aligned rows: K % 4 for A (and B^T), N % 4 for B.
+    const uintptr_t ptrs = (uintptr_t)g.a | (uintptr_t)g.b | (uintptr_t)g.b2;
+    const bool vec = (g.k % 4 == 0) && (g.lda % 4 == 0) && (g.ldb % 4 == 0) &&
+                     (BL == BL_NK || g.n % 4 == 0) && (ptrs & 15) == 0 &&
+                     (g.batch_a % 4 == 0) && (g.batch_b % 4 == 0);
+    const dim3 grid((uint32_t)nblocks, batch), block(512);
+    if (vec) hipLaunchKernelGGL((gemm_f32_kernel<2, true, BL, EPI, RMS>), grid, block, 0, s, g);
+    else hipLaunchKernelGGL((gemm_f32_kernel<2, false, BL, EPI, RMS>), grid, block, 0, s, g);
     MB_LAUNCH_CHECK("matmul_f32");
     return MB_OK;
 }
 
+}  // namespace
+
+GemmF32Args gemm_f32_args(const float* a, const float* b, float* c, uint32_t m, uint32_t n,
+                          uint32_t k) {
+    GemmF32Args g{};
+    g.a = a; g.b = b; g.c = c; g.m = m; g.n = n; g.k = k;
+    g.lda = k; g.ldb = n; g.ldc = n; g.ldr = n;
+    g.tiles_n = cdiv(n, BN);
+    return g;
+}
+
+int launch_gemm_f32_ex(GemmF32Args g, GemmF32Kind kind, uint32_t batch, hipStream_t s) {
+    if (g.m == 0 || g.n == 0 || batch == 0) return MB_OK;
+    if (!g.a || !g.b || !g.c || (kind == GEMM_F32_SWIGLU || kind == GEMM_F32_RMS_SWIGLU
+                                     ? !g.b2 : false) ||
+        (kind == GEMM_F32_RESID && !g.r))
+        return fail(MB_E_ARG, "matmul_f32: null pointer");
+    g.tiles_n = cdiv(g.n, BN);
+    switch (kind) {
+        case GEMM_F32_PLAIN: return launch_variant<BL_KN, EPI_STORE, false>(g, batch, s);
+        case GEMM_F32_RMS: return launch_variant<BL_KN, EPI_STORE, true>(g, batch, s);
+        case GEMM_F32_RMS_BT: return launch_variant<BL_NK, EPI_STORE, true>(g, batch, s);
+        case GEMM_F32_RESID: return launch_variant<BL_KN, EPI_RESID, false>(g, batch, s);
+        case GEMM_F32_SWIGLU: return launch_variant<BL_KN, EPI_SWIGLU, false>(g, batch, s);
+        case GEMM_F32_RMS_SWIGLU: return launch_variant<BL_KN, EPI_SWIGLU, true>(g, batch, s);
+    }
+    return fail(MB_E_ARG, "matmul_f32: unknown variant");
+}
+
+namespace {
+
+int launch_gemm_f32(const float* a, const float* b, float* c, uint32_t m, uint32_t n,
+                    uint32_t k, hipStream_t s) {
+    return launch_gemm_f32_ex(gemm_f32_args(a, b, c, m, n, k), GEMM_F32_PLAIN, 1, s);
+}
+
 // Registry launcher: A@0, B@1 (inputs f32), C@2 (output f32), M@3, N@4, K@5.
+// Also fused_qkv_projection (x @ W_qkv, the same bindings).
 int run_gemm_f32(const Bindings& bs, hipStream_t s, PartMarks*) {
     uint32_t m, n, k;
     int rc;
@@ -189,14 +284,86 @@ int run_gemm_f32(const Bindings& bs, hipStream_t s, PartMarks*) {
     return launch_gemm_f32((const float*)a, (const float*)b, (float*)c, m, n, k, s);
 }
 
+// batch_mm: A@0 [batch][M][K], B@1 [batch][K][N], C@2 [batch][M][N], M@3, N@4,
+// K@5.  The registry carries no batch scalar (the reference derives it from
+// the grid): it is A's size / (M K).
+int run_batch_mm(const Bindings& bs, hipStream_t s, PartMarks*) {
+    uint32_t m, n, k;
+    int rc;
+    if ((rc = bs.u32(3, &m, "M")) || (rc = bs.u32(4, &n, "N")) || (rc = bs.u32(5, &k, "K")))
+        return rc;
+    const uint64_t per_a = (uint64_t)m * k * 4;
+    if (per_a == 0) return fail(MB_E_ARG, "batch_matmul_f32: M and K must be positive");
+    const uint64_t batch = bs.nbytes(0) / per_a;
+    if (batch == 0 || batch * per_a != bs.nbytes(0))
+        return fail(MB_E_ARG, "batch_matmul_f32: A holds %llu bytes, not a multiple of M*K*4",
+                    (unsigned long long)bs.nbytes(0));
+    void *a, *b, *c;
+    if ((rc = bs.buffer(0, MB_DTYPE_F32, batch * per_a, false, &a, "A")) ||
+        (rc = bs.buffer(1, MB_DTYPE_F32, batch * k * n * 4, false, &b, "B")) ||
+        (rc = bs.buffer(2, MB_DTYPE_F32, batch * m * n * 4, true, &c, "C")))
+        return rc;
+    GemmF32Args g = gemm_f32_args((const float*)a, (const float*)b, (float*)c, m, n, k);
+    g.batch_a = (uint64_t)m * k;
+    g.batch_b = (uint64_t)k * n;
+    g.batch_c = (uint64_t)m * n;
+    return launch_gemm_f32_ex(g, GEMM_F32_PLAIN, (uint32_t)batch, s);
+}
+
+// rms_norm_linear: x@0 [M][K], W@1 [N][K], y@2 [M][N] = rmsnorm(x) W^T, M@3,
+// N@4, K@5, eps@6 (the reference Model hard-codes eps = 1e-5,
+// standard/rms_norm_linear.py:13; the registry passes the same value).
+int run_rms_norm_linear(const Bindings& bs, hipStream_t s, PartMarks*) {
+    uint32_t m, n, k;
+    float eps;
+    int rc;
+    if ((rc = bs.u32(3, &m, "M")) || (rc = bs.u32(4, &n, "N")) || (rc = bs.u32(5, &k, "K")) ||
+        (rc = bs.f32(6, &eps, "eps")))
+        return rc;
+    void *x, *w, *y;
+    if ((rc = bs.buffer(0, MB_DTYPE_F32, (uint64_t)m * k * 4, false, &x, "x")) ||
+        (rc = bs.buffer(1, MB_DTYPE_F32, (uint64_t)n * k * 4, false, &w, "W")) ||
+        (rc = bs.buffer(2, MB_DTYPE_F32, (uint64_t)m * n * 4, true, &y, "y")))
+        return rc;
+    GemmF32Args g = gemm_f32_args((const float*)x, (const float*)w, (float*)y, m, n, k);
+    g.ldb = k;
+    g.eps = eps;
+    return launch_gemm_f32_ex(g, GEMM_F32_RMS_BT, 1, s);
+}
+
+// swiglu: x@0 [M][K], W_gate@1 [K][N], W_up@2 [K][N], out@3 [M][N], M@4, N@5, K@6.
+int run_swiglu(const Bindings& bs, hipStream_t s, PartMarks*) {
+    uint32_t m, n, k;
+    int rc;
+    if ((rc = bs.u32(4, &m, "M")) || (rc = bs.u32(5, &n, "N")) || (rc = bs.u32(6, &k, "K")))
+        return rc;
+    void *x, *wg, *wu, *y;
+    if ((rc = bs.buffer(0, MB_DTYPE_F32, (uint64_t)m * k * 4, false, &x, "x")) ||
+        (rc = bs.buffer(1, MB_DTYPE_F32, (uint64_t)k * n * 4, false, &wg, "W_gate")) ||
+        (rc = bs.buffer(2, MB_DTYPE_F32, (uint64_t)k * n * 4, false, &wu, "W_up")) ||
+        (rc = bs.buffer(3, MB_DTYPE_F32, (uint64_t)m * n * 4, true, &y, "out")))
+        return rc;
+    GemmF32Args g = gemm_f32_args((const float*)x, (const float*)wg, (float*)y, m, n, k);
+    g.b2 = (const float*)wu;
+    return launch_gemm_f32_ex(g, GEMM_F32_SWIGLU, 1, s);
+}
+
 }  // namespace
 
 void register_gemm_f32() {
-    // Both names resolve to the same kernel: sqr_mm and rect_mm share the spec.
-    register_kernel({"sqr_matmul_f32", run_gemm_f32,
-                     reinterpret_cast<const void*>(&gemm_f32_kernel<2, true>), 1});
-    register_kernel({"rect_matmul_f32", run_gemm_f32,
-                     reinterpret_cast<const void*>(&gemm_f32_kernel<2, true>), 1});
+    const void* plain = reinterpret_cast<const void*>(
+        &gemm_f32_kernel<2, true, BL_KN, EPI_STORE, false>);
+    // sqr_mm, rect_mm and fused_qkv_projection share the plain GEMM's spec.
+    register_kernel({"sqr_matmul_f32", run_gemm_f32, plain, 1});
+    register_kernel({"rect_matmul_f32", run_gemm_f32, plain, 1});
+    register_kernel({"fused_qkv_projection_f32", run_gemm_f32, plain, 1});
+    register_kernel({"batch_matmul_f32", run_batch_mm, plain, 1});
+    register_kernel({"rms_norm_linear_f32", run_rms_norm_linear,
+                     reinterpret_cast<const void*>(&gemm_f32_kernel<2, true, BL_NK, EPI_STORE, true>),
+                     1});
+    register_kernel({"swiglu_f32", run_swiglu,
+                     reinterpret_cast<const void*>(&gemm_f32_kernel<2, true, BL_KN, EPI_SWIGLU, false>),
+                     1});
 }
 
 }  // namespace mb

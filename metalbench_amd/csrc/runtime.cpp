@@ -103,6 +103,7 @@ static std::vector<KernelEntry>& registry() {
         register_conv2d();
         register_gemm_bf16();
         register_decoder();
+        register_transformer_f32();
     });
     return table();
 }
@@ -137,6 +138,11 @@ int Bindings::buffer(uint32_t idx, uint32_t dtype, uint64_t min_bytes, bool outp
                     (unsigned long long)b->nbytes, (unsigned long long)min_bytes);
     *ptr = b->dev_ptr;
     return MB_OK;
+}
+
+uint64_t Bindings::nbytes(uint32_t idx) const {
+    const mb_binding* b = idx < 32 ? slot[idx] : nullptr;
+    return (b && b->role != MB_ROLE_SCALAR) ? b->nbytes : 0;
 }
 
 int Bindings::u32(uint32_t idx, uint32_t* v, const char* what) const {

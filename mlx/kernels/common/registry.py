@@ -129,3 +129,57 @@ conv2d("conv2d", 32, 56, 56, 64, 64, 3, 3, stride=1, pad=1, cpu_iters=20)
 # weights (reference registry.py:469-477).
 conv2d("conv2d_ref", 8, 64, 64, 64, 128, 3, 3, stride=1, pad=0,
        init_w=("normal", 0.0, 1.0))
+
+
+# ---- decoder sub-ops and adjacent GEMMs at the reference's own shapes --------
+
+# RMSNorm over rows of 1024 (reference registry.py:135-136, `reduction`
+# helper :79-98): x@0, y@1, cols@2, eps@3.  nn.RMSNorm's gain is all ones at
+# init, so y = x * rsqrt(mean(x^2) + eps).
+REGISTRY["rms_norm"] = dict(
+    metal_function="rms_norm_f32",
+    threadgroup=(1024, 1, 1),
+    input_bindings=(0,),
+    input_shapes=[(1024, 1024)],
+    output_shape=(1024, 1024),
+    rtol=1e-3, atol=1e-3,
+    grid=(1024, 1024, 1),
+    scalars=[dict(binding=2, dtype="u32", value=1024),
+             dict(binding=3, dtype="f32", value=1e-5)],
+    flops=1024 * 1024 * 5,
+    bytes=2 * 1024 * 1024 * 4,
+    model_kwargs=dict(dims=1024, eps=1e-5),
+)
+
+# Matrix-vector product y = A @ x, 1024 x 1024 (reference registry.py:151-162).
+REGISTRY["matvec"] = dict(
+    metal_function="matvec_f32",
+    threadgroup=(1024, 1, 1),
+    input_bindings=(0, 1),
+    input_shapes=[(1024, 1024), (1024,)],
+    output_shape=(1024,),
+    rtol=1e-3, atol=1e-3,
+    grid=(1024, 1024, 1),
+    scalars=[dict(binding=3, dtype="u32", value=1024)],
+    flops=2 * 1024 * 1024,
+    bytes=4 * (1024 * 1024 + 1024 + 1024),
+)
+
+# Batched GEMM C[b] = A[b] @ B[b]: 128 batches of 128 x 256 @ 256 x 512
+# (reference registry.py:61-77, 131): A@0, B@1, C@2, M@3, N@4, K@5.
+_BB, _BM, _BN, _BK = 128, 128, 512, 256
+REGISTRY["batch_mm"] = dict(
+    metal_function="batch_matmul_f32",
+    threadgroup=(512, 1, 1),
+    input_bindings=(0, 1),
+    input_shapes=[(_BB, _BM, _BK), (_BB, _BK, _BN)],
+    output_shape=(_BB, _BM, _BN),
+    rtol=1e-3, atol=1e-3,
+    grid=((_BN // 64) * 512, (_BM // 64) * _BB, 1),
+    scalars=[dict(binding=3, dtype="u32", value=_BM),
+             dict(binding=4, dtype="u32", value=_BN),
+             dict(binding=5, dtype="u32", value=_BK)],
+    flops=_BB * 2 * _BM * _BN * _BK,
+    bytes=_BB * 4 * (_BM * _BK + _BK * _BN + _BM * _BN),
+    compute_dtype="f32",
+)

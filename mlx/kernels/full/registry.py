@@ -51,3 +51,28 @@ REGISTRY["llama_decoder_step"] = dict(
     model_kwargs=dict(B=_B, D=_D, H=_H, H_kv=_HKV, FF=_FF, L=_L, base=500000.0, eps=1e-5),
     cpu_iters=3,
 )
+
+# ---- LLaMA decoder layer, prefill, the reference's own shape (fp32) ------------
+# S 64 tokens at positions 0..63, D 128, 4 query heads / 2 KV heads (Dh 32),
+# SwiGLU FFN 256, RoPE base 10000, RMSNorm eps 1e-5, full (non-causal)
+# attention; all inputs normal(0, 1) (reference registry.py:87-104).
+REGISTRY["llama_decoder_layer"] = dict(
+    metal_function="llama_decoder_layer_f32",
+    threadgroup=(256, 1, 1),
+    input_bindings=(0, 1, 2, 3, 4),
+    input_shapes=[(64, 128), (128, 128 + 2 * 2 * 32), (128, 128), (128, 2 * 256), (256, 128)],
+    output_shape=(64, 128),
+    rtol=1e-2, atol=1e-2,
+    grid=(1024, 1, 1),
+    scalars=[dict(binding=6, dtype="u32", value=64),
+             dict(binding=7, dtype="u32", value=128),
+             dict(binding=8, dtype="u32", value=4),
+             dict(binding=9, dtype="u32", value=2),
+             dict(binding=10, dtype="u32", value=256),
+             dict(binding=11, dtype="f32", value=10000.0),
+             dict(binding=12, dtype="f32", value=1e-5)],
+    flops=64 * (128 * 256 * 2 + 64 * 128 * 2 + 128 * 128 * 2 + 128 * 512 * 2 + 256 * 128 * 2),
+    bytes=4 * (64 * 128 * 3 + 128 * 256 + 128 * 128 + 128 * 512 + 256 * 128),
+    compute_dtype="f32",
+    model_kwargs=dict(S=64, D=128, H=4, H_kv=2, FF=256, base=10000.0, eps=1e-5),
+)

@@ -24,6 +24,13 @@ How each function is pinned (tests/test_oracle.py):
   silu / swiglu        silu(0) = 0, scipy.special.expit form
   llama_decoder_step   zero weights -> y = x; L = 0 equals the S = 1 prefill
   llama_decoder_layer  zero weights -> y = x; S = 1 reduces to v @ W_o path
+  fused_add_rms_norm   residual 0 -> rms_norm(x); x = -residual -> 0
+  rms_norm_linear      W = I -> rms_norm(x); brute-force loops
+  swiglu               zero gate or up weights -> 0; brute-force loops
+  llama_attention      S = 1 closed form (v @ W_o); brute-force per-head
+                       loops; equals the decoder layer's attention half
+  rope_embedding       rope_interleaved over rows at positions 0..S-1
+  matvec / batch_mm    brute-force loops; per-batch 2-D matmul
 """
 from __future__ import annotations
 
@@ -213,3 +220,52 @@ def llama_decoder_layer(x, w_qkv, w_o, w_gu, w_down, *, n_heads, n_kv_heads, bas
     h2 = rms_norm(x1, eps)
     gu = h2 @ np.asarray(w_gu, np.float64)
     return x1 + (silu(gu[:, :ff_dim]) * gu[:, ff_dim:]) @ np.asarray(w_down, np.float64)
+
+
+# ---- decoder sub-ops at the reference's own shapes -----------------------------------
+
+
+def fused_add_rms_norm(x, residual, eps: float = 1e-5) -> np.ndarray:
+    """RMSNorm(x + residual), unit gain (reference
+    mlx/kernels/standard/fused_add_rms_norm.py:11-12)."""
+    return rms_norm(np.asarray(x, np.float64) + np.asarray(residual, np.float64), eps)
+
+
+def rms_norm_linear(x, w, eps: float = 1e-5) -> np.ndarray:
+    """rms_norm(x) @ w.T, w [out][in] (reference
+    mlx/kernels/standard/rms_norm_linear.py:12-14)."""
+    return rms_norm(x, eps) @ np.asarray(w, np.float64).T
+
+
+def swiglu(x, w_gate, w_up) -> np.ndarray:
+    """silu(x @ W_gate) * (x @ W_up) (reference mlx/kernels/standard/swiglu.py:9-10)."""
+    x = np.asarray(x, np.float64)
+    return silu(x @ np.asarray(w_gate, np.float64)) * (x @ np.asarray(w_up, np.float64))
+
+
+def rope_embedding(x, base: float = 10000.0) -> np.ndarray:
+    """Rows of x (S, D) rotated at positions 0..S-1 with omega_i = 1 / base^(2i/D)
+    (reference mlx/kernels/standard/rope_embedding.py:15-32)."""
+    x = np.asarray(x, np.float64)
+    return rope_interleaved(x, np.arange(x.shape[0], dtype=np.float64), base)
+
+
+def llama_attention(x, w_qkv, w_o, *, n_heads, n_kv_heads, base=10000.0):
+    """GQA attention with RoPE, no cache, no mask, no norm or residual
+    (reference mlx/kernels/standard/llama_attention.py:30-58): qkv = x W_qkv,
+    q and k rotated at positions 0..S-1, query head h reads kv head h // G,
+    softmax over all S keys, heads concatenated and projected by W_o."""
+    x = np.asarray(x, np.float64)
+    s_len, d = x.shape
+    dh = d // n_heads
+    g = n_heads // n_kv_heads
+    qkv = x @ np.asarray(w_qkv, np.float64)
+    pos = np.arange(s_len, dtype=np.float64)
+    out = np.empty((s_len, d))
+    for h in range(n_heads):
+        kvh = h // g
+        q = rope_interleaved(qkv[:, h * dh:(h + 1) * dh], pos, base)
+        k = rope_interleaved(qkv[:, d + kvh * dh:d + (kvh + 1) * dh], pos, base)
+        v = qkv[:, d + (n_kv_heads + kvh) * dh:d + (n_kv_heads + kvh + 1) * dh]
+        out[:, h * dh:(h + 1) * dh] = softmax(q @ k.T / np.sqrt(dh), axis=-1) @ v
+    return out @ np.asarray(w_o, np.float64)

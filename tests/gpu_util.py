@@ -56,3 +56,24 @@ def assert_close(actual, expected, rtol, atol, what=""):
         raise AssertionError(f"{what}: {int(bad.sum())} / {a.size} elements out of tolerance "
                              f"(rtol={rtol}, atol={atol}); worst at {idx}: got {a[idx]!r}, "
                              f"expected {e[idx]!r}, max |diff| {diff.max():.3e}")
+
+
+def run_bound(metal_function: str, inputs, outputs, scalars, dtype="f32"):
+    """Run a registry kernel through mb_run with explicit bindings (shapes the
+    registry does not hold).  inputs: [(binding, tensor)], outputs:
+    [(binding, shape)], scalars: [(binding, dtype, value)].  Returns the
+    outputs as CPU tensors."""
+    native.init(0)
+    dev = torch.device("cuda", 0)
+    d_in = [(b, t.to(dev)) for b, t in inputs]
+    d_out = [(b, torch.full(tuple(shape), float("nan"), dtype=torch.float32, device=dev))
+             for b, shape in outputs]
+    sync()
+    binds = [native.make_binding(b, native.ROLE_INPUT, dtype, t.data_ptr(),
+                                 t.numel() * t.element_size()) for b, t in d_in]
+    binds += [native.make_binding(b, native.ROLE_OUTPUT, dtype, t.data_ptr(),
+                                  t.numel() * t.element_size()) for b, t in d_out]
+    binds += [native.make_binding(b, native.ROLE_SCALAR, dt, value=v) for b, dt, v in scalars]
+    native.run(native.kernel_find(metal_function), binds, 0, 1, native.RUN_SYNC_EACH)
+    sync()
+    return [t.cpu() for _, t in d_out]

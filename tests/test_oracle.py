@@ -259,6 +259,122 @@ def test_decoder_layer_zero_weights_is_identity():
     assert np.array_equal(y, x)
 
 
+# ---- decoder sub-ops at the reference shapes ---------------------------------------------
+
+def test_fused_add_rms_norm_closed_forms():
+    x, r = rnd(5, 16), rnd(5, 16)
+    assert np.allclose(oracle.fused_add_rms_norm(x, np.zeros_like(x), 1e-5), oracle.rms_norm(x, 1e-5))
+    assert np.array_equal(oracle.fused_add_rms_norm(x, -x, 1e-5), np.zeros_like(x))
+    # commutes in its two inputs, and unit output RMS when eps is negligible
+    assert np.allclose(oracle.fused_add_rms_norm(x, r, 0.0), oracle.fused_add_rms_norm(r, x, 0.0))
+    y = oracle.fused_add_rms_norm(x, r, 0.0)
+    assert np.allclose(np.sqrt(np.mean(y * y, axis=-1)), 1.0)
+
+
+def _brute_rms_row(row, eps):
+    ms = sum(v * v for v in row) / len(row)
+    return [v / (ms + eps) ** 0.5 for v in row]
+
+
+def test_rms_norm_linear_identity_and_brute_force():
+    x = rnd(3, 6)
+    assert np.allclose(oracle.rms_norm_linear(x, np.eye(6), 1e-5), oracle.rms_norm(x, 1e-5))
+    w = rnd(4, 6)   # [out][in]
+    got = oracle.rms_norm_linear(x, w, 1e-5)
+    for i in range(3):
+        n = _brute_rms_row(list(x[i]), 1e-5)
+        for o in range(4):
+            assert abs(got[i, o] - sum(n[k] * w[o, k] for k in range(6))) < 1e-12
+
+
+def test_swiglu_zero_weights_and_brute_force():
+    x, wg, wu = rnd(3, 5), rnd(5, 4), rnd(5, 4)
+    assert np.array_equal(oracle.swiglu(x, wg, np.zeros_like(wu)), np.zeros((3, 4)))
+    assert np.array_equal(oracle.swiglu(x, np.zeros_like(wg), wu), np.zeros((3, 4)))
+    got = oracle.swiglu(x, wg, wu)
+    for i in range(3):
+        for j in range(4):
+            g = sum(x[i, k] * wg[k, j] for k in range(5))
+            u = sum(x[i, k] * wu[k, j] for k in range(5))
+            assert abs(got[i, j] - g * scipy.special.expit(g) * u) < 1e-12
+
+
+def test_rope_embedding_rows_at_positions():
+    x = rnd(6, 8)
+    y = oracle.rope_embedding(x, 10000.0)
+    assert np.array_equal(y[0], x[0])                       # position 0: identity
+    for p in range(6):                                      # complex multiply, omega = 1/base^(2i/D)
+        w = 1.0 / 10000.0 ** (2.0 * np.arange(4) / 8)
+        z = (x[p, 0::2] + 1j * x[p, 1::2]) * np.exp(1j * p * w)
+        assert np.allclose(y[p, 0::2], z.real) and np.allclose(y[p, 1::2], z.imag)
+
+
+def _brute_attention(x, w_qkv, w_o, H, HKV, base):
+    """Pure-Python loops: every head, query and key, math.exp softmax."""
+    import math
+    S, D = x.shape
+    dh, g = D // H, H // HKV
+    qkv = [[sum(x[i, k] * w_qkv[k, j] for k in range(D)) for j in range(w_qkv.shape[1])]
+           for i in range(S)]
+
+    def rot(vec, pos):
+        out = list(vec)
+        for i in range(len(vec) // 2):
+            a = pos / base ** (2.0 * i / len(vec))
+            out[2 * i] = vec[2 * i] * math.cos(a) - vec[2 * i + 1] * math.sin(a)
+            out[2 * i + 1] = vec[2 * i] * math.sin(a) + vec[2 * i + 1] * math.cos(a)
+        return out
+
+    att = [[0.0] * D for _ in range(S)]
+    for h in range(H):
+        kvh = h // g
+        for i in range(S):
+            q = rot(qkv[i][h * dh:(h + 1) * dh], i)
+            sc = []
+            for j in range(S):
+                k = rot(qkv[j][D + kvh * dh:D + (kvh + 1) * dh], j)
+                sc.append(sum(a * b for a, b in zip(q, k)) / math.sqrt(dh))
+            mx = max(sc)
+            e = [math.exp(v - mx) for v in sc]
+            z = sum(e)
+            for d in range(dh):
+                att[i][h * dh + d] = sum(e[j] / z * qkv[j][D + (HKV + kvh) * dh + d]
+                                         for j in range(S))
+    return np.array([[sum(att[i][k] * w_o[k, j] for k in range(D)) for j in range(D)]
+                     for i in range(S)])
+
+
+def test_llama_attention_brute_force_and_single_token():
+    S, D, H, HKV = 3, 8, 4, 2
+    x, wqkv, wo = rnd(S, D), rnd(D, D + 2 * HKV * (D // H)), rnd(D, D)
+    got = oracle.llama_attention(x, wqkv, wo, n_heads=H, n_kv_heads=HKV, base=100.0)
+    assert np.allclose(got, _brute_attention(x, wqkv, wo, H, HKV, 100.0), rtol=1e-10, atol=1e-10)
+    # one token: softmax over one key is 1, RoPE at position 0 is the identity,
+    # so every head h outputs v of kv head h // G and y = that @ W_o
+    x1 = x[:1]
+    v = (x1 @ wqkv)[:, D + HKV * 2:]
+    heads = np.concatenate([v[:, (h // (H // HKV)) * 2:(h // (H // HKV)) * 2 + 2] for h in range(H)], 1)
+    assert np.allclose(oracle.llama_attention(x1, wqkv, wo, n_heads=H, n_kv_heads=HKV), heads @ wo)
+
+
+def test_llama_attention_is_the_decoder_layers_attention_half():
+    S, D, H, HKV, FF = 5, 16, 4, 2, 8
+    x, wqkv, wo = rnd(S, D), rnd(D, D + 2 * HKV * (D // H)), rnd(D, D)
+    zero_gu, zero_dn = np.zeros((D, 2 * FF)), np.zeros((FF, D))
+    layer = oracle.llama_decoder_layer(x, wqkv, wo, zero_gu, zero_dn, n_heads=H, n_kv_heads=HKV)
+    attn = oracle.llama_attention(oracle.rms_norm(x, 1e-5), wqkv, wo, n_heads=H, n_kv_heads=HKV)
+    assert np.allclose(layer, x + attn)
+
+
+def test_matvec_and_batch_mm():
+    a, v = rnd(4, 5), rnd(5)
+    assert np.allclose(oracle.matmul(a, v), [sum(a[i, k] * v[k] for k in range(5)) for i in range(4)])
+    A, B = rnd(3, 2, 4), rnd(3, 4, 5)
+    got = oracle.matmul(A, B)
+    for b in range(3):
+        assert np.allclose(got[b], oracle.matmul(A[b], B[b]))
+
+
 # ---- planted mistakes: the checks above must catch plausible oracle bugs -----------------
 
 def test_planted_mistakes_are_caught(monkeypatch):
