@@ -65,15 +65,23 @@ def _work(name: str, meta: dict):
         parts = _decoder_part_bytes()
         return dict(part="gate_up_swiglu", bound="hbm", per_launch=parts["gate_up_swiglu"],
                     parts=parts)
-    if meta.get("flops", 0) == 0:
+    if _bound(meta) == "hbm":
         return dict(part=None, bound="hbm", per_launch=int(meta["bytes"]))
     return dict(part=None, bound="mfma", per_launch=int(meta["flops"]))
+
+
+def _bound(meta: dict) -> str:
+    """HBM if the registry's arithmetic intensity is below the MI355X ridge
+    point for its compute dtype (peak flops / 8 TB/s), else MFMA."""
+    flops, nbytes = meta.get("flops", 0), meta.get("bytes", 1)
+    ridge = MFMA_PEAK_TFLOPS[meta.get("compute_dtype", "f32")] * 1e12 / (HBM_PEAK_GBPS * 1e9)
+    return "hbm" if flops / nbytes < ridge else "mfma"
 
 
 def _value_unit(name: str, meta: dict, ms_per_step: float):
     if name == "llama_decoder_step":
         return ms_per_step * 1000.0, "us/step", False
-    if meta.get("flops", 0) == 0:
+    if _bound(meta) == "hbm":
         return meta["bytes"] / (ms_per_step * 1e-3) / 1e9, "GB/s", True
     return meta["flops"] / (ms_per_step * 1e-3) / 1e12, "TFLOP/s", True
 
@@ -164,6 +172,25 @@ def _cpu_baseline(name: str, inputs, meta: dict) -> dict:
         sec, n = timed(lambda: oracle.conv2d_nhwc(x, w, 1, 1), max_iters=3)
         return {"value": meta["flops"] / sec / 1e12, "unit": "TFLOP/s", "cores": _blas_threads(),
                 "kind": "port", "sample": f"full conv2d in float64 numpy, median of {n}"}
+    generic = {   # the other registry entries: the full workload through its oracle
+        "rect_mm": lambda a: oracle.matmul(*a),
+        "batch_mm": lambda a: oracle.matmul(*a),
+        "matvec": lambda a: oracle.matmul(*a),
+        "fused_qkv_projection": lambda a: oracle.matmul(*a),
+        "rms_norm": lambda a: oracle.rms_norm(a[0], 1e-5),
+        "fused_add_rms_norm": lambda a: oracle.fused_add_rms_norm(a[0], a[1], 1e-5),
+        "rms_norm_linear": lambda a: oracle.rms_norm_linear(a[0], a[1], 1e-5),
+        "rope_embedding": lambda a: oracle.rope_embedding(a[0], 10000.0),
+        "swiglu": lambda a: oracle.swiglu(*a),
+        "llama_attention": lambda a: oracle.llama_attention(*a, n_heads=4, n_kv_heads=2),
+        "llama_decoder_layer": lambda a: oracle.llama_decoder_layer(*a, n_heads=4, n_kv_heads=2),
+    }
+    if name in generic:
+        args = [f(t) for t in inputs]
+        sec, n = timed(lambda: generic[name](args), max_iters=5)
+        value, unit, _ = _value_unit(name, meta, sec * 1e3)
+        return {"value": value, "unit": unit, "cores": _blas_threads(), "kind": "port",
+                "sample": f"full workload in float64 numpy, median of {n}"}
     if name == "large_mm":
         rows = 512
         a = f(inputs[0][:rows])
