@@ -23,6 +23,7 @@ from __future__ import annotations
 import argparse
 import datetime as _dt
 import json
+import os
 import sys
 from pathlib import Path
 
@@ -157,7 +158,7 @@ def evaluate(name, *, seed, warmup, iters, dry_run=False, profile=False, solo=No
     speedup = (r_t["median_ms"] / k_t["median_ms"]) if k_t["median_ms"] > 0 else float("inf")
     metrics = _kernel_metrics({"speedup": speedup})
 
-    return {
+    result = {
         "task": name,
         "chip": chip,
         "metal_device": k_t.get("hip_device", "unknown"),
@@ -171,6 +172,68 @@ def evaluate(name, *, seed, warmup, iters, dry_run=False, profile=False, solo=No
         "outputs": per_output,
         "compute_dtype": b.compute_dtype,
     }
+    # The reference host always emits a profiling block (main.mm:183-195);
+    # with --profile it holds counters, here from rocprofv3 passes.
+    result["profiling"] = profile_counters(name, seed) if profile else {"counters_available": False}
+    return result
+
+
+# ---- --profile: hardware counters through rocprofv3 --------------------------------------
+# The reference samples MTLCounterSet around one extra dispatch (reference
+# harness.py:401-402, main.mm:53-72).  Here the same registry kernel is run
+# once more in a child process under `rocprofv3 --pmc`, one pass per counter
+# group (a pass may hold at most 8 SQ, 4 TCC and 2 GRBM counters; FETCH_SIZE
+# takes 3 TCC and WRITE_SIZE 2, so they go in separate passes), and the values
+# are summed over the kernels of that one dispatch.
+PROFILE_PASSES = (
+    ("GRBM_GUI_ACTIVE", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_INSTS_MFMA",
+     "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE",
+     "SQ_WAIT_INST_LDS", "SQ_WAIT_INST_ANY", "FETCH_SIZE"),
+    ("WRITE_SIZE",),
+)
+
+
+def parse_counter_csv(path) -> dict:
+    """Sum each counter over this library's kernels in a rocprofv3
+    counter_collection.csv."""
+    import csv
+    out = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            if "mb::" not in r.get("Kernel_Name", ""):
+                continue
+            out[r["Counter_Name"]] = out.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    return out
+
+
+def profile_counters(name, seed, timeout_s=120) -> dict:
+    import shutil
+    import subprocess
+    import tempfile
+    exe = shutil.which("rocprofv3")
+    if not exe:
+        return {"counters_available": False, "reason": "rocprofv3 not found"}
+    env = dict(os.environ, TMPDIR="/tmp")
+    values = {}
+    for counters in PROFILE_PASSES:
+        with tempfile.TemporaryDirectory(dir="/tmp") as d:
+            cmd = [exe, "--pmc", *counters, "-f", "csv", "-d", d, "-o", "prof", "--",
+                   sys.executable, str(H.REPO_ROOT / "mlx" / "scripts" / "harness.py"), name,
+                   "--metal-only", "--warmup", "0", "--iters", "1", "--seed", str(seed),
+                   "--no-session"]
+            try:
+                r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout_s,
+                                   cwd="/tmp", env=env)
+            except subprocess.TimeoutExpired:
+                return {"counters_available": False, "reason": f"rocprofv3 pass timed out ({counters[0]} ...)"}
+            found = list(Path(d).rglob("*counter_collection.csv"))
+            if r.returncode != 0 or not found:
+                return {"counters_available": False,
+                        "reason": f"rocprofv3 exit {r.returncode}: {r.stderr.strip()[-200:]}"}
+            values.update(parse_counter_csv(found[0]))
+    names = [c for p in PROFILE_PASSES for c in p]
+    return {"counters_available": True, "counter_set": "rocprofv3 --pmc (" + ", ".join(names) + ")",
+            "samples": [{"name": c, "value": int(values.get(c, 0))} for c in names]}
 
 
 # Each target picks ONE primary metric to optimize (reference harness.py:176-186).
@@ -322,6 +385,13 @@ def _print_report(result, target, score):
         pass
     for p in k_t.get("parts", []):
         print(f"    part {p['name']:24s} {p['median_ms']*1000:8.1f} µs")
+    prof = result.get("profiling", {})
+    if prof.get("counters_available"):
+        print(f"  profiling   : {prof['counter_set']}")
+        for smp in prof.get("samples", []):
+            print(f"    {smp['name']:40s} {smp['value']}")
+    elif prof.get("reason"):
+        print(f"  profiling   : unavailable ({prof['reason']})")
     print()
     print(f"  {'target':>10s}   {'score':>10s}")
     print(f"  {'-'*10}   {'-'*10}")
@@ -331,44 +401,11 @@ def _print_report(result, target, score):
     print(line)
 
 
-def _update_best_times_md(session_path=None, out_path=None):
-    """Regenerate best_times.md from session.json (reference harness.py:336-384)."""
-    sp = Path(session_path) if session_path else H.SESSION_PATH
-    if not sp.exists():
-        return
-    session = json.loads(sp.read_text())
-
-    def _type(name):
-        if "mm" in name or "matmul" in name:
-            return "matmul"
-        if "transpose" in name:
-            return "copy"
-        if "conv" in name:
-            return "conv"
-        if "decoder" in name:
-            return "model"
-        return "?"
-
-    chip_order = sorted(session.keys())
-    chip_header = " | ".join(f"{c} HIP | {c} speedup" for c in chip_order)
-    lines = ["# MetalBench Best Times (gfx950 backend)", "",
-             f"| kernel | type | {chip_header} |",
-             "|---|" + "|---|" * (len(chip_order) * 2 + 1)]
-    all_names = set()
-    for cdata in session.values():
-        all_names.update(cdata.keys())
-    for name in sorted(all_names):
-        cols = [name, _type(name)]
-        for chip in chip_order:
-            d = session[chip].get(name, {})
-            ms, spd = d.get("best_time_ms"), d.get("speedup_vs_mlx")
-            cols.append(f"{ms:.3f}ms" if ms else "--")
-            cols.append(f"{spd:.1f}×" if spd else "--")
-        lines.append("| " + " | ".join(cols) + " |")
-    lines += ["", "---", f"**Chips:** {', '.join(chip_order)}", "",
-              "Speedup is against the CPU spec on the host cores (MLX is not available)."]
-    (Path(out_path) if out_path else H.REPO_ROOT / "best_times.md").write_text(
-        "\n".join(lines) + "\n")
+def _update_best_times_md(session_path=None, out_dir=None):
+    """Regenerate best_times.md and LINK.md from session.json (reference
+    harness.py:336-384, scripts/render_best_times.py, scripts/render_link_md.py)."""
+    from . import render
+    return render.update_markdown(session_path, out_dir)
 
 
 def main(argv=None):
@@ -382,7 +419,7 @@ def main(argv=None):
                     help="iterations of the CPU spec timing (default: registry cpu_iters)")
     ap.add_argument("--dry-run", action="store_true")
     ap.add_argument("--profile", action="store_true",
-                    help="record the request; counters come from rocprofv3 around this run")
+                    help="hardware counters of one extra dispatch, from rocprofv3 --pmc passes")
     ap.add_argument("--save", action="store_true",
                     help="save full result JSON to results/<chip>/<name>.json")
     ap.add_argument("--no-session", action="store_true", help="don't update session.json")

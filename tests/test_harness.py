@@ -82,9 +82,22 @@ def test_session_update_rules(tmp_path):
     assert rec["metal_source_path"].endswith("transpose.hip")
     assert harness.update_session("transpose_2d", _fake_result(True, 0.3), "speed", 10, sp)[0] is False
     assert harness.update_session("transpose_2d", _fake_result(True, 0.1), "speed", 10, sp)[0] is True
-    md = tmp_path / "best_times.md"
-    harness._update_best_times_md(sp, md)
-    assert "transpose_2d" in md.read_text() and "0.100ms" in md.read_text()
+    assert harness._update_best_times_md(sp, tmp_path)
+    best = (tmp_path / "best_times.md").read_text()
+    row = next(line for line in best.splitlines() if line.startswith("| `transpose_2d` |"))
+    cells = [c.strip() for c in row.strip("|").split("|")]
+    # reference scripts/render_best_times.py format: kernel | set | chips..., "ms (speedup×)"
+    header = next(line for line in best.splitlines() if line.startswith("| kernel | set |"))
+    chips = [c.strip() for c in header.strip("|").split("|")][2:]
+    assert chips[0] == "amd-instinct-mi355x" and chips[1:] == ["M1", "M2", "M3", "M4", "M5"]
+    assert cells[:2] == ["`transpose_2d`", "common"]
+    assert cells[2] == f"0.100 ({74.5 / 0.1:.2f}×)" and cells[3:] == ["—"] * 5
+    link = (tmp_path / "LINK.md").read_text()
+    assert "## amd-instinct-mi355x\n" in link and "## apple-m2 _(no data)_" in link
+    # every kernel with data links to the HIP file that registers it
+    target = link.split("[transpose_2d](")[1].split(")")[0]
+    assert target == "metalbench_amd/csrc/transpose.hip" and (REPO / target).is_file()
+    assert "- [llama_decoder_layer](metalbench_amd/csrc/transformer_f32.hip)" in link
 
 
 def test_grade_targets():
@@ -116,3 +129,25 @@ def test_cli_dry_run_and_cpu_only():
                         "--iters", "2"], cwd=REPO, capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
     assert "mlx ref     :" in r.stdout
+
+
+def test_profile_counter_parsing_and_absent_profiler(tmp_path, monkeypatch):
+    csv_path = tmp_path / "p_counter_collection.csv"
+    csv_path.write_text(
+        "Dispatch_Id,Kernel_Name,Counter_Name,Counter_Value\n"
+        '1,"void mb::(anonymous namespace)::skinny_gemm_kernel<0, 4>(...)",FETCH_SIZE,100.5\n'
+        "2,void mb::(anonymous namespace)::attention_kernel<4>(...),FETCH_SIZE,50\n"
+        "3,at::native::vectorized_elementwise_kernel,FETCH_SIZE,7\n"
+        "2,void mb::(anonymous namespace)::attention_kernel<4>(...),GRBM_GUI_ACTIVE,9\n")
+    got = harness.parse_counter_csv(csv_path)
+    assert got == {"FETCH_SIZE": 150.5, "GRBM_GUI_ACTIVE": 9.0}   # torch's kernel excluded
+    # one pass may hold at most 8 SQ, 4 TCC (FETCH_SIZE 3, WRITE_SIZE 2) and 2 GRBM counters
+    for p in harness.PROFILE_PASSES:
+        sq = sum(c.startswith("SQ_") for c in p)
+        tcc = 3 * ("FETCH_SIZE" in p) + 2 * ("WRITE_SIZE" in p)
+        grbm = sum(c.startswith("GRBM_") for c in p)
+        assert sq <= 8 and tcc <= 4 and grbm <= 2, p
+    import shutil
+    monkeypatch.setattr(shutil, "which", lambda name: None)
+    prof = harness.profile_counters("sqr_mm", 0)
+    assert prof["counters_available"] is False and "rocprofv3" in prof["reason"]
