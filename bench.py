@@ -92,7 +92,8 @@ def _roofline(name: str, w: dict, k_t: dict, compute_dtype: str) -> dict:
         mean_ms = part["mean_ms"]
         kernel = w["part"]
     else:
-        mean_ms = k_t["mean_ms"]
+        # single-kernel workload: average launch duration over the timed region
+        mean_ms = k_t.get("device_ms_per_launch", k_t["mean_ms"])
         kernel = None
     sec = mean_ms * 1e-3
     if w["bound"] == "hbm":
@@ -279,6 +280,8 @@ def _mean_timing(runs: list) -> dict:
 
 
 def _run_workload(name, steps, warmup, want_cpu):
+    import ctypes
+
     import torch
 
     from metalbench_amd import helpers as H
@@ -318,18 +321,27 @@ def _run_workload(name, steps, warmup, want_cpu):
                 launch(i % R)
         else:
             native.run(kid, bind_sets[0], 0, warmup, native.RUN_PIPELINED)
-    # Timed region: exactly `steps` launches back to back, no events in the
-    # stream, bracketed by synchronize on both sides.
+    # Timed region: exactly `steps` launches back to back, bracketed by
+    # synchronize on both sides and by a hipEvent pair on the stream the
+    # kernels run on (the library enqueues on torch's current stream here), so
+    # the device time per launch is measured over the same region.
+    stream = torch.cuda.Stream()   # default priority; a real (non-null) stream handle
+    native.load().mb_set_stream(ctypes.c_void_p(stream.cuda_stream))
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev0.record(stream)
     if launch:
         for i in range(steps):
             launch(i % R)
     else:
         native.run(kid, bind_sets[0], 0, steps, native.RUN_WALL_ONLY)
+    ev1.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1000.0
     ms_per_step = wall_ms / steps
+    device_ms = ev0.elapsed_time(ev1) / steps
+    native.load().mb_set_stream(None)
     # Per-kernel durations (roofline): `steps` more steps with a hipEvent pair
     # per step and a mark before each kernel of the step; rotating workloads
     # run them one by one over the copies, so each is timed cold as well.
@@ -341,6 +353,7 @@ def _run_workload(name, steps, warmup, want_cpu):
         k_t = native.run(kid, bind_sets[0], 0, steps, native.RUN_PIPELINED | native.RUN_PARTS)
     torch.cuda.synchronize()
 
+    k_t["device_ms_per_launch"] = device_ms
     w = _work(name, meta)
     value, unit, hib = _value_unit(name, meta, ms_per_step)
     rec = {"value": value, "unit": unit, "higher_is_better": hib, "ms_per_step": ms_per_step,

@@ -35,6 +35,7 @@ void clear_error();
 // ---- library state ----------------------------------------------------------
 bool initialized();
 hipStream_t stream_or_default(void* s);   // NULL -> current library stream
+uint32_t device_cu_count();               // compute units of the initialised device
 
 // Library-owned device workspace, grown on demand, freed by mb_shutdown().
 // The first `zero_prefix` bytes are guaranteed zero the first time they are

@@ -41,10 +41,13 @@ struct State {
     void* ws = nullptr;
     size_t ws_bytes = 0;
     size_t ws_zeroed = 0;   // bytes at the front of ws known to be zero
+    uint32_t cu_count = 0;
 };
 static State g;
 
 bool initialized() { return g.inited; }
+
+uint32_t device_cu_count() { return g.cu_count; }
 
 hipStream_t stream_or_default(void* s) {
     if (s) return static_cast<hipStream_t>(s);
@@ -211,6 +214,7 @@ int mb_init(int ordinal) {
     MB_HIP_TRY(hipSetDevice(ordinal));
     MB_HIP_TRY(hipStreamCreate(&g.lib_stream));
     g.device = ordinal;
+    g.cu_count = (uint32_t)p.multiProcessorCount;
     g.inited = true;
     (void)registry();
     return MB_OK;

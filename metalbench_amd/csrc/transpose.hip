@@ -5,20 +5,27 @@
 // binding 1, scalars rows@2 and cols@3, rtol = atol = 0).
 //
 // gfx950 design (HBM bound, 0 flops, 2*rows*cols*4 algorithmic bytes):
-//  * persistent workgroups (two per CU, 256 threads) walk 128x128 tiles
+//  * persistent workgroups, one per CU (256 threads), walk 128x128 tiles
 //    (64 KB) in column-major tile order, so concurrently running workgroups
-//    write adjacent 512-byte pieces of the same rows of B;
+//    write adjacent 512-byte pieces of the same rows of B.  One workgroup per
+//    CU beats two (5.7 vs 5.5 TB/s cold): fewer concurrent streams, better
+//    DRAM page locality;
+//  * when every tile is full, each workgroup keeps three tiles in registers:
+//    two tiles' loads stay in flight while the third is transposed and
+//    stored (transpose_full_kernel);
 //  * global reads: 32 lanes load a 512-byte row segment of A as float4 (16
 //    loads per lane), non-temporal: each byte is read once;
 //  * the tile goes through LDS as float[128][129]: the +1 column of padding
 //    makes both the row-wise writes and the column-wise reads conflict free
 //    (bank = (row + col) mod 64);
-//  * the next tile's loads are issued right after the LDS write of the
-//    current one, so they are in flight while it is read back and stored;
+//  * otherwise (transpose_2d_f32_kernel) the next tile's loads are issued
+//    right after the LDS write of the current one, so they are in flight
+//    while it is read back and stored;
 //  * global writes: 32 lanes store a 512-byte row segment of B as float4,
 //    non-temporal (the output is streamed, never re-read here).  Cold (working
-//    set rotated past the 256 MB memory-side cache) this moves ~5.4 TB/s on
-//    MI355X, against ~4.9 TB/s with cached loads and stores;
+//    set rotated past the 256 MB memory-side cache) the full-tile kernel moves
+//    ~5.8 TB/s on MI355X (72 % of 8 TB/s); a plain non-temporal copy of the
+//    same bytes moves 6.4 TB/s;
 //  * tiles that run past the edge, rows or cols not multiples of 4, or
 //    pointers that are not 16-byte aligned take a guarded scalar path, so any
 //    shape (including empty and ragged ones) is handled.
@@ -36,7 +43,6 @@ constexpr int THREADS = 256;
 constexpr int LPR = TILE / 4;             // lanes per 512-byte row segment
 constexpr int RPI = THREADS / LPR;        // rows per load instruction (workgroup-wide)
 constexpr int NI = TILE / RPI;            // float4 per lane per tile
-constexpr uint32_t MAX_GRID = 512;        // two workgroups per CU
 
 __global__ __launch_bounds__(THREADS)
 void transpose_2d_f32_kernel(const float* __restrict__ a, float* __restrict__ b,
@@ -105,6 +111,60 @@ void transpose_2d_f32_kernel(const float* __restrict__ a, float* __restrict__ b,
     }
 }
 
+// Every tile full (rows, cols multiples of TILE; 16-byte aligned): three
+// register tile buffers per thread, the loads of the next two tiles in flight
+// while one tile goes through LDS and out.
+__global__ __launch_bounds__(THREADS, 2)
+void transpose_full_kernel(const float* __restrict__ a, float* __restrict__ b, uint32_t rows,
+                           uint32_t cols, uint32_t tiles_r, uint32_t ntiles) {
+    __shared__ float tile[TILE][TILE + 1];
+    const uint32_t tx = threadIdx.x % LPR, ty = threadIdx.x / LPR;
+    const uint32_t G = gridDim.x, t0 = blockIdx.x;
+    const uint32_t nk = t0 < ntiles ? (ntiles - t0 + G - 1) / G : 0;   // tiles of this workgroup
+    f32x4 v0[NI], v1[NI], v2[NI];
+    auto load = [&](f32x4 (&v)[NI], uint32_t k) {
+        const uint32_t t = t0 + k * G;
+        const uint32_t r0 = (t % tiles_r) * TILE, c0 = (t / tiles_r) * TILE;
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            v[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(
+                a + (size_t)(r0 + ty + RPI * i) * cols + c0 + 4 * tx));
+    };
+    auto process = [&](f32x4 (&v)[NI], uint32_t k) {
+        const uint32_t t = t0 + k * G;
+        const uint32_t r0 = (t % tiles_r) * TILE, c0 = (t / tiles_r) * TILE;
+        __syncthreads();   // the previous tile's LDS reads are done
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) tile[ty + RPI * i][4 * tx + e] = v[i][e];
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const uint32_t j = ty + RPI * i;   // row of B inside the tile
+            const f32x4 o = {tile[4 * tx + 0][j], tile[4 * tx + 1][j], tile[4 * tx + 2][j],
+                             tile[4 * tx + 3][j]};
+            __builtin_nontemporal_store(
+                o, reinterpret_cast<f32x4*>(b + (size_t)(c0 + j) * rows + r0 + 4 * tx));
+        }
+    };
+    if (nk > 0) load(v0, 0);
+    if (nk > 1) load(v1, 1);
+    if (nk > 2) load(v2, 2);
+    for (uint32_t k = 0; k < nk; k += 3) {
+        process(v0, k);
+        if (k + 3 < nk) load(v0, k + 3);
+        if (k + 1 < nk) {
+            process(v1, k + 1);
+            if (k + 4 < nk) load(v1, k + 4);
+        }
+        if (k + 2 < nk) {
+            process(v2, k + 2);
+            if (k + 5 < nk) load(v2, k + 5);
+        }
+    }
+}
+
 int launch_transpose(const float* a, float* b, uint32_t rows, uint32_t cols, hipStream_t s) {
     if (rows == 0 || cols == 0) return MB_OK;
     if (!a || !b) return fail(MB_E_ARG, "transpose_2d_f32: null pointer");
@@ -112,7 +172,13 @@ int launch_transpose(const float* a, float* b, uint32_t rows, uint32_t cols, hip
     const uint64_t ntiles = (uint64_t)tiles_r * tiles_c;
     if (ntiles > 0x7fffffffull) return fail(MB_E_ARG, "transpose_2d_f32: shape too large");
     const uint32_t vec_ok = ((rows | cols) & 3) == 0 && (((uintptr_t)a | (uintptr_t)b) & 15) == 0;
-    const uint32_t grid = (uint32_t)std::min<uint64_t>(ntiles, MAX_GRID);
+    const uint32_t grid = (uint32_t)std::min<uint64_t>(ntiles, std::max(device_cu_count(), 1u));
+    if (vec_ok && rows % TILE == 0 && cols % TILE == 0) {
+        hipLaunchKernelGGL(transpose_full_kernel, dim3(grid), dim3(THREADS), 0, s, a, b, rows, cols,
+                           tiles_r, (uint32_t)ntiles);
+        MB_LAUNCH_CHECK("transpose_2d_f32");
+        return MB_OK;
+    }
     hipLaunchKernelGGL(transpose_2d_f32_kernel, dim3(grid), dim3(THREADS), 0, s, a, b, rows,
                        cols, tiles_r, (uint32_t)ntiles, vec_ok);
     MB_LAUNCH_CHECK("transpose_2d_f32");
@@ -136,7 +202,7 @@ int run_transpose(const Bindings& bs, hipStream_t s, PartMarks*) {
 
 void register_transpose() {
     register_kernel({"transpose_2d_f32", run_transpose,
-                     reinterpret_cast<const void*>(&transpose_2d_f32_kernel), 1});
+                     reinterpret_cast<const void*>(&transpose_full_kernel), 1});
 }
 
 }  // namespace mb
