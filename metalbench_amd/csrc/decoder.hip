@@ -22,8 +22,8 @@
 //                     the splits and the new token (log-sum-exp);
 //   3. wo_residual    skinny GEMM attn @ W_o, finisher adds x, writes x1
 //                     (fp32 + bf16) and per-tile sums of x1^2;
-//   4. gate_up_swiglu skinny GEMM x1 @ [W_gate | W_up], each tile holding 64
-//                     gate and the matching 64 up columns, finisher applies
+//   4. gate_up_swiglu skinny GEMM x1 @ [W_gate | W_up], each tile holding 256
+//                     gate and the matching 256 up columns, finisher applies
 //                     the RMSNorm scale and silu(g) * u;
 //                     x1 and the SwiGLU output feed the next GEMMs as hi + lo
 //                     bf16 pairs (two MFMAs), so their bf16 rounding does not
@@ -32,20 +32,14 @@
 // RMSNorm is a per-row scale, so (r x) W = r (x W): it is applied to the GEMM
 // outputs instead of materialising h / h2.
 //
-// Skinny GEMM (M = batch <= 16): a workgroup owns a 128-column tile and one
-// K split.  The weights are row-major [K][N] (x @ W), but the MFMA operand
-// wants 8 consecutive k per lane, so each lane loads an 8(k) x 8(n) block as
-// eight 16-byte rows (one 256-byte row segment per 16 lanes), transposes it in
-// registers with v_perm_b32 and stores eight K-contiguous 16-byte chunks into
-// LDS (pitch 136 bf16, chunk index XOR-swizzled by (row / 16) so both the
-// stores and the ds_read_b128 operand reads are bank-conflict free).  The
-// activations are the MFMA A operand (16 rows = the batch, zero-filled above
-// it), parked in LDS before the weights arrive.  Weights are loaded
-// non-temporal (each byte is read once per step).
-// v_mfma_f32_16x16x32_bf16 accumulates; split-K
-// partials go to the workspace and the LAST workgroup of each column tile (an
-// atomic counter, reset by that workgroup) sums them and runs the epilogue;
-// the partials travel through device-coherent (sc1) accesses, not fences.
+// Skinny GEMM (M = batch <= 16): about one workgroup per CU, each owning a
+// column tile and one K split, streams its weights through a ring of register
+// slots straight into the MFMA B operand (an 8 x 8 register transpose, no LDS
+// on the weight path); weights are loaded non-temporal (each byte is read
+// once per step).  Split-K partials go to the workspace and the LAST
+// workgroup of each column tile (an atomic counter, reset by that workgroup)
+// sums them in split order and runs the epilogue; the partials travel through
+// device-coherent (sc1) accesses, not fences.  Details at skinny_gemm_kernel.
 #include "common.h"
 
 #include <math.h>
@@ -61,23 +55,35 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int DH = 128;        // head_dim (fixed)
 constexpr int MROWS = 16;      // MFMA rows = max batch
-constexpr int BN = 128;        // skinny GEMM column tile
-constexpr int KS = 128;        // k rows per LDS step
-constexpr int WP = KS + 8;     // LDS pitch (bf16) of one transposed weight column
+constexpr int BN = 128;        // skinny GEMM column tile (W_gate | W_up: up to 4 x BN)
+constexpr int KS = 128;        // K split granularity (rows)
+constexpr int RING = 2;        // skinny GEMM: units in flight per workgroup
 constexpr int MAXG = 16;       // query heads per kv head (MFMA columns)
+constexpr float LOG2E = 1.4426950408889634f;
 
 enum { EPI_QKV = 0, EPI_WO = 1, EPI_GU = 2, EPI_DOWN = 3 };
 
-__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
-__device__ __forceinline__ uint16_t f2bf(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Two floats -> a packed bf16 pair (a in the low half), round to nearest even
+// (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
-__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+// hi + lo bf16 terms of a pair: hi = bf16(v), lo = bf16(v - hi).
+__device__ __forceinline__ void split_bf16(float a, float b, uint32_t& hi, uint32_t& lo) {
+    hi = pack_bf16(a, b);
+    lo = pack_bf16(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
+}
+
+// silu(v) = v / (1 + e^-v) with the hardware exp2 and reciprocal (about 1 ulp
+// each); e^-v overflowing to inf gives v * 0 = -0 for very negative v.
+__device__ __forceinline__ float silu(float v) {
+    return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-v * LOG2E));
+}
 
 // ---- cross-workgroup hand-off without L2 flushes ---------------------------------
 // MI355X has one L2 per XCD; an agent-scope fence (__threadfence) writes back
@@ -111,6 +117,15 @@ __device__ __forceinline__ float ld_sc1(__amdgpu_buffer_rsrc_t r, uint32_t off) 
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CPOL_SC1));
 }
 
+// A workgroup-uniform pointer or size, kept in SGPRs (buffer descriptors built
+// from it then need no waterfall loop around each load).
+__device__ __forceinline__ void* uniform_ptr(const void* ptr) {
+    const uint64_t v = reinterpret_cast<uint64_t>(ptr);
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<void*>((hi << 32) | lo);
+}
+
 // Signal "my sc1 stores are done" and return true in the workgroup that
 // completes `target` arrivals on `counter` (which it resets for the next use).
 __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t target, uint32_t* s_flag) {
@@ -135,7 +150,7 @@ struct StepParams {
     const uint16_t *x, *k_cache, *v_cache;
     uint16_t *y, *k_new, *v_new;
     uint32_t* attn_counters;   // [B * Hkv]
-    float* partial;            // split-K partials [tiles * splits][BN][16] (column-major tile)
+    float* partial;            // split-K partials [tiles * splits][16][tile columns]
     uint32_t partial_bytes;
     float* sumsq;              // [qkv tiles * splits][16] sum of x^2 over each split
     uint16_t* q;               // [B][D] rotated queries * 1/sqrt(Dh), bf16 (MFMA operand)
@@ -162,238 +177,283 @@ struct GemmCfg {
     uint32_t* counters;    // [tiles]
 };
 
-__device__ __forceinline__ uint32_t tile_col(const GemmCfg& g, const StepParams& p, uint32_t tile,
-                                             uint32_t c) {
-    if (!g.paired) return tile * BN + c;
-    return c < 64 ? tile * 64 + c : p.ff + tile * 64 + (c - 64);
-}
-
 // ---- skinny GEMM + split-K finisher --------------------------------------------------
 
-// A workgroup owns one 128-column tile and one K split of NSTEPS x 128 rows
-// (NSTEPS = 1, 2 or 4).  The step is HBM bound with long memory latency under
-// load, so what matters is bytes in flight per CU:
-//   1. the split's activation slice (16 rows x NSTEPS*128, hi and lo terms) is
-//      loaded first and parked in LDS, so the MFMA A fragments come from LDS
-//      (lgkmcnt) and never sit in the vmcnt queue ahead of weight data;
-//   2. then ALL of the split's weight loads are issued at once (NSTEPS x 32 KB
-//      per workgroup, two workgroups per CU);
-//   3. step s waits only for its own weight rows (vmcnt = 8 x steps still in
-//      flight behind them), transposes them through LDS and runs its MFMAs.
-// sched_barrier keeps the compiler from interleaving these groups, because
-// vmcnt retires loads in issue order.
-template <int EPI, int NSTEPS>
-__global__ __launch_bounds__(256, 2)
+// C[16][N] = A[16][K] W[K][N]: A = the batch's activations (rows past the
+// batch read as zero), W row-major.  A workgroup owns a column tile of
+// TBN = 128 * WW columns and a K split of kc rows.  Its four waves stand WW
+// side by side in N (128 columns each) and 4 / WW deep in K (32 rows each), so
+// one unit of the split is (128 / WW) rows x TBN columns = 32 KB of weights;
+// WW = 4 makes every row segment a workgroup reads 1 KB long (512 B per half
+// for the paired gate | up tile), which HBM streams markedly faster than 256
+// or 128 B segments.
+//
+// The weights never touch LDS.  Lane (kq = lane / 16, nl = lane % 16) of a
+// wave loads rows 8 kq .. 8 kq + 7 of the wave's 32-row slab, columns
+// 8 nl .. 8 nl + 7 of its 128-column slab (eight 16-byte loads; a load
+// instruction covers 256 contiguous bytes of four rows), and transposes the
+// 8 x 8 block in registers with v_perm_b32 into eight 8-k vectors, one per
+// column 8 nl + c.  Vector c is the B operand of v_mfma_f32_16x16x32_bf16 for
+// the 16 columns {8 nl + c | nl < 16} (lane group kq = k octet kq); the A
+// operand, activation row nl and k octet kq, is one 16-byte load per lane.
+// A unit is therefore 8 MFMAs per wave (16 with hi + lo activations), and
+// accumulator c holds rows 4 kq .. 4 kq + 3 of column 8 nl + c.
+//
+// Units stream through a ring of R register slots: consuming unit j waits
+// for its slot only (vmcnt = the younger slots still in flight), transposes
+// it and re-issues the slot for unit j + R before running the MFMAs, so R
+// units stay in flight through the whole split.  Every load is a buffer
+// load clipped to the split: weight rows past it, and activation chunks past
+// it or past the batch, return zeros without touching memory, so the ring
+// runs a fixed number of units (a multiple of R) with one load order and
+// no branches.  sched_barrier keeps the compiler from interleaving the slots'
+// loads, because vmcnt retires loads in issue order.
+//
+// After the K loop the accumulators meet in LDS as a row-major [16][TBN] tile
+// (the 4 / WW row groups summed); the split-K partial in the workspace has the
+// same layout (one coalesced sc1 store per float4).  The last workgroup of
+// the tile (atomic counter) sums the other splits' partials, with the
+// epilogue's own inputs loaded in the same round trip, and runs the epilogue.
+template <int TBN>
+__device__ __forceinline__ uint32_t tile_col(const GemmCfg& g, const StepParams& p, uint32_t tile,
+                                             uint32_t c) {
+    if (!g.paired) return tile * TBN + c;
+    return c < TBN / 2 ? tile * (TBN / 2) + c : p.ff + tile * (TBN / 2) + (c - TBN / 2);
+}
+
+template <int EPI, int WW, int R>
+__global__ __launch_bounds__(256, 1)
 void skinny_gemm_kernel(GemmCfg g, StepParams p) {
     constexpr bool SPLIT_A = (EPI == EPI_GU || EPI == EPI_DOWN);   // hi + lo activations
     constexpr int NTERMS = SPLIT_A ? 2 : 1;
-    constexpr int KC = NSTEPS * KS;                 // k rows of this split
-    constexpr int AP = KC + 8;                      // LDS pitch (bf16) of an activation row
-    constexpr int ACH = MROWS * KC / 8 / 256;       // 16-byte activation chunks per thread per term
+    constexpr int TBN = 128 * WW;                 // tile columns
+    constexpr int RG = 4 / WW;                    // waves stacked in K
+    constexpr int UR = 32 * RG;                   // k rows per unit
+    constexpr int NQ = MROWS * TBN / 4 / 256;     // float4s of the tile per thread
+    static_assert(WW == 1 || EPI == EPI_GU, "QKV, WO and DOWN epilogues use 128-column tiles");
 
-    __shared__ __attribute__((aligned(16))) uint16_t wt[BN * WP];
-    __shared__ __attribute__((aligned(16))) uint16_t as[NTERMS][MROWS * AP];
-    float* red = reinterpret_cast<float*>(wt);   // finisher sums, after the K loop
+    // RG accumulator tiles, then 16 x 16 floats of row-statistics scratch
+    __shared__ __attribute__((aligned(16))) float red[RG * MROWS * TBN + MROWS * 16];
     __shared__ float red_ss[MROWS];
     __shared__ uint32_t s_last;
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t cw = wave % WW, rw = wave / WW;       // wave's column slab, row slab
+    const uint32_t kq = lane >> 4, nl = lane & 15;
     const uint32_t tile = blockIdx.x % g.tiles;
     const uint32_t split = blockIdx.x / g.tiles;
-    const uint32_t k_begin = split * KC;
+    const uint32_t k_begin = split * g.kc;
+    const uint32_t k_rows = min(g.kc, g.k - k_begin);   // a multiple of 128
 
-    // ---- 1. activations -> registers (issued first) ----
-    // chunk q (0 .. 16*KC/8): row q / (KC/8), k octet q % (KC/8)
-    u32x4 ar[NTERMS][ACH];
+    // ---- the ring ----
+    const uint32_t a_bytes = __builtin_amdgcn_readfirstlane(p.batch * g.lda * 2);
+    const __amdgpu_buffer_rsrc_t ars0 =
+        __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(g.a), 0, a_bytes, RSRC_FLAGS);
+    const __amdgpu_buffer_rsrc_t ars1 = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(SPLIT_A ? g.a_lo : g.a), 0, a_bytes, RSRC_FLAGS);
+    const uint32_t a_voff = (nl * g.lda + k_begin + 32 * rw + 8 * kq) * 2;
+    const bool a_row_ok = nl < p.batch;
+    const uint32_t ldw2 = g.ldw * 2;
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(g.w + (size_t)k_begin * g.ldw), 0, __builtin_amdgcn_readfirstlane(k_rows * ldw2),
+        RSRC_FLAGS);
+    const uint32_t w_voff = (32 * rw + 8 * kq) * ldw2 + tile_col<TBN>(g, p, tile, 128 * cw + 8 * nl) * 2;
+
+    u32x4 ra[R][NTERMS];
+    u32x4 rw8[R][8];
+    auto issue = [&](int s, uint32_t j) {
+        const uint32_t ao = (a_row_ok && j * UR < k_rows) ? a_voff + j * UR * 2 : 0x80000000u;
+        ra[s][0] = __builtin_amdgcn_raw_buffer_load_b128(ars0, ao, 0, 0);
+        if (SPLIT_A) ra[s][NTERMS - 1] = __builtin_amdgcn_raw_buffer_load_b128(ars1, ao, 0, 0);
+        const uint32_t wo = w_voff + j * UR * ldw2;
 #pragma unroll
-    for (int t = 0; t < NTERMS; ++t) {
-        const uint16_t* src = t == 0 ? g.a : g.a_lo;
+        for (int i = 0; i < 8; ++i)   // streamed once per step
+            rw8[s][i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wo + i * ldw2, 0, CPOL_NT);
+    };
 #pragma unroll
-        for (int i = 0; i < ACH; ++i) {
-            const uint32_t q = tid + 256 * i, row = q / (KC / 8), oct = q % (KC / 8);
-            const bool ok = row < p.batch;
-            // rows past the batch read row 0 (valid) and are zeroed
-            const u32x4 v = *reinterpret_cast<const u32x4*>(
-                src + (size_t)(ok ? row : 0) * g.lda + k_begin + 8 * oct);
-            ar[t][i] = ok ? v : u32x4{};
-        }
+    for (int s = 0; s < R; ++s) {
+        issue(s, s);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- 2. every weight load of the split ----
-    const uint32_t co = tid & 15, ko = tid >> 4;
-    const uint16_t* wp = g.w + (size_t)(k_begin + 8 * ko) * g.ldw + tile_col(g, p, tile, 8 * co);
-    u32x4 r[NSTEPS][8];
-#pragma unroll
-    for (int s = 0; s < NSTEPS; ++s)
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            r[s][i] = __builtin_nontemporal_load(   // streamed once per step
-                reinterpret_cast<const u32x4*>(wp + (size_t)(s * KS + i) * g.ldw));
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- epilogue inputs, in case this workgroup finishes the tile ----
-    // (issued behind the weights, so no weight wait grows; the finisher then
-    // needs one memory round trip, for the other splits' partials)
-    const uint32_t eb = tid >> 4, ec = 8 * (tid & 15);   // epilogue: row eb, columns ec .. ec+7
-    u32x4 pre_x = {};                                    // WO: x (bf16)
-    f32x4 pre_x1[2] = {f32x4{}, f32x4{}};                // DOWN: x1 (fp32)
-    float pre_ss[8] = {};                                // GU: sumsq2 terms, see finish_rows
-    if (EPI == EPI_WO)
-        pre_x = *reinterpret_cast<const u32x4*>(p.x + (size_t)(eb < p.batch ? eb : 0) * p.d +
-                                                tile * BN + ec);
-    if (EPI == EPI_DOWN) {
-        const float* src = p.x1 + (size_t)(eb < p.batch ? eb : 0) * p.d + tile * BN + ec;
-        pre_x1[0] = *reinterpret_cast<const f32x4*>(src);
-        pre_x1[1] = *reinterpret_cast<const f32x4*>(src + 4);
+    // QKV: the RoPE rotation of pair (2i, 2i+1), i = tid % 64, at position
+    // cache_len, computed while the first loads are in flight
+    float rope_cs = 1.f, rope_sn = 0.f;
+    if (EPI == EPI_QKV) {
+        const float omega = powf(p.rope_base, -2.0f * (float)(tid & 63) / (float)DH);
+        sincosf((float)p.cache_len * omega, &rope_sn, &rope_cs);
     }
-    if (EPI == EPI_GU) {
-        const uint32_t ntile = p.d / BN;
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-            pre_ss[u] = p.sumsq2[min(eb + 16u * u, ntile - 1) * MROWS + (tid & 15)];
-    }
-    __builtin_amdgcn_sched_barrier(0);
 
-    // ---- activations -> LDS (they are the oldest loads) ----
+    f32x4 acc[8];
 #pragma unroll
-    for (int t = 0; t < NTERMS; ++t)
-#pragma unroll
-        for (int i = 0; i < ACH; ++i) {
-            const uint32_t q = tid + 256 * i, row = q / (KC / 8), oct = q % (KC / 8);
-            *reinterpret_cast<u32x4*>(&as[t][row * AP + 8 * oct]) = ar[t][i];
-        }
-    __builtin_amdgcn_sched_barrier(0);
-
-    const uint32_t arow = lane & 15, agrp = lane >> 4;
-    f32x4 acc[2] = {f32x4{}, f32x4{}};
+    for (int c = 0; c < 8; ++c) acc[c] = f32x4{};
     float ss = 0.f;
+    const uint32_t trips = (g.kc / UR + R - 1) / R;
 
-    // ---- 3. steps ----
+    for (uint32_t t = 0; t < trips; ++t) {
 #pragma unroll
-    for (int s = 0; s < NSTEPS; ++s) {
-        // 8x8 transpose of this lane's block: LDS row (8co + c) = weight
-        // column, 16-byte chunk ko (XOR-swizzled by row/16) = k octet.
+        for (int s = 0; s < R; ++s) {
+            // 8x8 transpose: b[c] = column 8 nl + c, k = 8 kq .. 8 kq + 7
+            bf16x8 b[8];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            uint32_t lo[4], hi[4];
+            for (int m = 0; m < 4; ++m) {
+                u32x4 lo, hi;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                lo[j] = __builtin_amdgcn_perm(r[s][2 * j + 1][m], r[s][2 * j][m], 0x05040100u);
-                hi[j] = __builtin_amdgcn_perm(r[s][2 * j + 1][m], r[s][2 * j][m], 0x07060302u);
+                for (int j = 0; j < 4; ++j) {
+                    lo[j] = __builtin_amdgcn_perm(rw8[s][2 * j + 1][m], rw8[s][2 * j][m], 0x05040100u);
+                    hi[j] = __builtin_amdgcn_perm(rw8[s][2 * j + 1][m], rw8[s][2 * j][m], 0x07060302u);
+                }
+                b[2 * m] = __builtin_bit_cast(bf16x8, lo);
+                b[2 * m + 1] = __builtin_bit_cast(bf16x8, hi);
             }
-            const uint32_t row0 = 8 * co + 2 * m, row1 = row0 + 1;
-            *reinterpret_cast<u32x4*>(wt + row0 * WP + 8 * (ko ^ ((row0 >> 4) & 7))) =
-                u32x4{lo[0], lo[1], lo[2], lo[3]};
-            *reinterpret_cast<u32x4*>(wt + row1 * WP + 8 * (ko ^ ((row1 >> 4) & 7))) =
-                u32x4{hi[0], hi[1], hi[2], hi[3]};
-        }
-        __syncthreads();
-        bf16x8 a[4], alo[4];
+            const bf16x8 a = __builtin_bit_cast(bf16x8, ra[s][0]);
+            const bf16x8 alo = __builtin_bit_cast(bf16x8, ra[s][NTERMS - 1]);
+            // slot s is free: its next unit's loads go out now
+            __builtin_amdgcn_sched_barrier(0);
+            issue(s, (t + 1) * R + s);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            const uint32_t ao = arow * AP + s * KS + 32 * kb + 8 * agrp;
-            a[kb] = *reinterpret_cast<const bf16x8*>(&as[0][ao]);
-            if (SPLIT_A) alo[kb] = *reinterpret_cast<const bf16x8*>(&as[NTERMS - 1][ao]);
-        }
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-            const uint32_t row = (wave * 2 + cb) * 16 + (lane & 15);
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-                const uint32_t chunk = (4 * kb + agrp) ^ ((row >> 4) & 7);
-                const bf16x8 bfrag = *reinterpret_cast<const bf16x8*>(wt + row * WP + 8 * chunk);
-                acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[kb], bfrag, acc[cb], 0, 0, 0);
+            for (int c = 0; c < 8; ++c) {
+                acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[c], acc[c], 0, 0, 0);
                 if (SPLIT_A)
-                    acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo[kb], bfrag, acc[cb], 0,
-                                                                       0, 0);
+                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo, b[c], acc[c], 0, 0, 0);
             }
-        }
-        if (EPI == EPI_QKV && wave == 0) {   // RMSNorm statistics from the A operand
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
+            if (EPI == EPI_QKV) {   // RMSNorm statistics from the A operand
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float v = (float)a[kb][e];
+                    const float v = (float)a[e];
                     ss += v * v;
                 }
+            }
         }
-        __syncthreads();
     }
 
-    // Split-K partial, column-major per tile: lane holds rows 4*agrp .. +3 of
-    // column (wave*2 + cb)*16 + lane%16 -> one 16-byte sc1 store.
-    const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(p.partial, p.partial_bytes);
-    const uint32_t part_base = (tile * g.splits + split) * (MROWS * BN * 4);
+    // ---- accumulators -> row-major [16][TBN] tile in LDS, row groups summed ----
+    {
+        float* buf = red + rw * (MROWS * TBN);
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-        const uint32_t c = (wave * 2 + cb) * 16 + (lane & 15);
-        st_sc1(prs, part_base + (c * MROWS + 4 * agrp) * 4, acc[cb]);
+        for (int r = 0; r < 4; ++r) {
+            float* dst = buf + (4 * kq + r) * TBN + 128 * cw + 8 * nl;
+            *reinterpret_cast<f32x4*>(dst) = f32x4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+            *reinterpret_cast<f32x4*>(dst + 4) = f32x4{acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
+        }
     }
-    const __amdgpu_buffer_rsrc_t srs = coherent_rsrc(p.sumsq, p.sumsq_bytes);
-    if (EPI == EPI_QKV && wave == 0) {
+    if (EPI == EPI_QKV) {   // sum of x^2 per row over this split: lanes nl of every kq and wave
         ss += __shfl_xor(ss, 16);
         ss += __shfl_xor(ss, 32);
-        if (lane < 16) st_sc1(srs, ((tile * g.splits + split) * MROWS + lane) * 4, ss);
+        if (lane < 16) red[RG * MROWS * TBN + wave * MROWS + lane] = ss;
+    }
+    __syncthreads();
+    f32x4 v[NQ];
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) {
+        const uint32_t q = tid + 256 * h;
+        v[h] = reinterpret_cast<const f32x4*>(red)[q];
+#pragma unroll
+        for (int r = 1; r < RG; ++r) v[h] += reinterpret_cast<const f32x4*>(red + r * MROWS * TBN)[q];
+    }
+
+    // split-K partial: the same row-major tile, float4 q at byte 16 q
+    constexpr uint32_t SPLIT_BYTES = MROWS * TBN * 4;
+    const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(p.partial, p.partial_bytes);
+    const uint32_t tile_base = tile * g.splits * SPLIT_BYTES;
+#pragma unroll
+    for (int h = 0; h < NQ; ++h) st_sc1(prs, tile_base + split * SPLIT_BYTES + (tid + 256 * h) * 16, v[h]);
+    const __amdgpu_buffer_rsrc_t srs = coherent_rsrc(p.sumsq, p.sumsq_bytes);
+    if (EPI == EPI_QKV && tid < MROWS) {
+        const float* sp = red + RG * MROWS * TBN;
+        st_sc1(srs, ((tile * g.splits + split) * MROWS + tid) * 4,
+               sp[tid] + sp[MROWS + tid] + sp[2 * MROWS + tid] + sp[3 * MROWS + tid]);
     }
     if (!arrive_last(&g.counters[tile], g.splits, &s_last)) return;
 
     // ---- finisher: this workgroup is the last of its tile ----
-    // float4 q of a tile = column q/4, rows 4*(q%4) .. +3; sum over the splits
-    // with eight splits' loads in flight together (past the last split the
-    // last one is re-read and dropped, so no load sits behind a branch).
-    {
-        constexpr uint32_t SPLIT_BYTES = MROWS * BN * 4, SB = 8;
-        const uint32_t tile_base = tile * g.splits * SPLIT_BYTES;
-        f32x4 v0 = {}, v1 = {};
-        for (uint32_t sp0 = 0; sp0 < g.splits; sp0 += SB) {
-            f32x4 a[SB], b[SB];
+    // One memory round trip: the first SB splits' partials, the QKV split sums
+    // of x^2 and the epilogue's inputs are all issued before the first wait.
+    // Partials and sums are read through descriptors clipped to this tile's
+    // splits, so loads past the last split return zeros and every load and
+    // add is unconditional (a load behind a branch would cost a round trip of
+    // its own).  Splits are summed in split order whichever workgroup
+    // finishes, so the result does not depend on arrival order.
+    constexpr uint32_t SB = NQ >= 8 ? 4 : 8;   // splits per batch of partial loads
+    constexpr uint32_t UT = 8;                 // QKV: x^2 sums per thread per batch
+    const __amdgpu_buffer_rsrc_t trs = coherent_rsrc(
+        reinterpret_cast<const uint8_t*>(p.partial) + tile_base, g.splits * SPLIT_BYTES);
+    const __amdgpu_buffer_rsrc_t qrs =
+        coherent_rsrc(p.sumsq + tile * g.splits * MROWS, g.splits * MROWS * 4);
+    const uint32_t row = tid & 15, grp = tid >> 4;   // row statistics: row, group of splits
+    f32x4 w[SB][NQ];
 #pragma unroll
-            for (uint32_t u = 0; u < SB; ++u) {
-                const uint32_t o = tile_base + min(sp0 + u, g.splits - 1) * SPLIT_BYTES;
-                a[u] = ld4_sc1(prs, o + tid * 16);
-                b[u] = ld4_sc1(prs, o + (256 + tid) * 16);
-            }
+    for (uint32_t u = 0; u < SB; ++u)
+#pragma unroll
+        for (int h = 0; h < NQ; ++h) w[u][h] = ld4_sc1(trs, u * SPLIT_BYTES + (tid + 256 * h) * 16);
+    float xs[UT] = {};
+    if (EPI == EPI_QKV) {
+#pragma unroll
+        for (uint32_t u = 0; u < UT; ++u) xs[u] = ld_sc1(qrs, ((grp + 16 * u) * MROWS + row) * 4);
+    }
+    const uint32_t eb = tid >> 4, ec = 8 * (tid & 15);   // epilogue: row eb, columns ec .. ec+7
+    u32x4 pre_x = {};                                    // WO: x (bf16)
+    f32x4 pre_x1[2] = {f32x4{}, f32x4{}};                // DOWN: x1 (fp32)
+    float pre_ss[8] = {};                                // GU: x1^2 sums of the W_o tiles
+    if (EPI == EPI_WO)
+        pre_x = *reinterpret_cast<const u32x4*>(p.x + (size_t)(eb < p.batch ? eb : 0) * p.d +
+                                                tile * TBN + ec);
+    if (EPI == EPI_DOWN) {
+        const float* src = p.x1 + (size_t)(eb < p.batch ? eb : 0) * p.d + tile * TBN + ec;
+        pre_x1[0] = *reinterpret_cast<const f32x4*>(src);
+        pre_x1[1] = *reinterpret_cast<const f32x4*>(src + 4);
+    }
+    if (EPI == EPI_GU) {
+        const uint32_t ntile = p.d / 128;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            pre_ss[u] = p.sumsq2[min(eb + 16u * u, ntile - 1) * MROWS + (tid & 15)];
+    }
+    {
+        f32x4 sum[NQ];
+#pragma unroll
+        for (int h = 0; h < NQ; ++h) {
+            sum[h] = w[0][h];
+#pragma unroll
+            for (uint32_t u = 1; u < SB; ++u) sum[h] += w[u][h];
+        }
+        for (uint32_t sp0 = SB; sp0 < g.splits; sp0 += SB) {   // more than SB splits
 #pragma unroll
             for (uint32_t u = 0; u < SB; ++u)
-                if (sp0 + u < g.splits) { v0 += a[u]; v1 += b[u]; }
-        }
-        // red is row-major [16][BN] for the epilogues
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t q = tid + 256 * h, c = q >> 2, r0 = 4 * (q & 3);
-            const f32x4 v = h ? v1 : v0;
+                for (int h = 0; h < NQ; ++h)
+                    w[u][h] = ld4_sc1(trs, (sp0 + u) * SPLIT_BYTES + (tid + 256 * h) * 16);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) red[(r0 + e) * BN + c] = v[e];
+            for (uint32_t u = 0; u < SB; ++u)
+#pragma unroll
+                for (int h = 0; h < NQ; ++h) sum[h] += w[u][h];
         }
+#pragma unroll
+        for (int h = 0; h < NQ; ++h) reinterpret_cast<f32x4*>(red)[tid + 256 * h] = sum[h];
     }
-    // Row statistics, thread (row = tid % 16, group = tid / 16) summing every
-    // 16th term, then the 16 groups through LDS:
-    //   QKV: sum of x^2 over the splits (sc1 loads, all in flight together);
-    //   GU:  sum of x1^2 over the W_o column tiles (prefetched) -> RMSNorm scale.
+    // Row statistics, thread (row, grp) summing every 16th term, then the 16
+    // groups through LDS:
+    //   QKV: sum of x^2 over the splits;
+    //   GU:  sum of x1^2 over the W_o column tiles -> RMSNorm scale.
     if (EPI == EPI_QKV || EPI == EPI_GU) {
-        float* scratch = red + MROWS * BN;   // 16 x 16 floats past the tile sums
-        const uint32_t row = tid & 15, grp = tid >> 4;
-        float v = 0.f;
+        float* scratch = red + MROWS * TBN;   // 16 x 16 floats past the tile sums
+        float sv = 0.f;
         if (EPI == EPI_QKV) {
-            constexpr uint32_t UT = 8;
-            for (uint32_t t0 = 0; t0 < g.splits; t0 += 16 * UT) {
-                float x[UT];
 #pragma unroll
-                for (uint32_t u = 0; u < UT; ++u) {
-                    const uint32_t t = min(t0 + grp + 16 * u, g.splits - 1);
-                    x[u] = ld_sc1(srs, ((tile * g.splits + t) * MROWS + row) * 4);
-                }
+            for (uint32_t u = 0; u < UT; ++u) sv += xs[u];
+            for (uint32_t t0 = 16 * UT; t0 < g.splits; t0 += 16 * UT) {   // more than 128 splits
 #pragma unroll
                 for (uint32_t u = 0; u < UT; ++u)
-                    if (t0 + grp + 16 * u < g.splits) v += x[u];
+                    xs[u] = ld_sc1(qrs, ((t0 + grp + 16 * u) * MROWS + row) * 4);
+#pragma unroll
+                for (uint32_t u = 0; u < UT; ++u) sv += xs[u];
             }
         } else {
 #pragma unroll
             for (uint32_t u = 0; u < 8; ++u)
-                if (grp + 16 * u < p.d / BN) v += pre_ss[u];
+                if (grp + 16 * u < p.d / 128) sv += pre_ss[u];
         }
-        scratch[grp * MROWS + row] = v;
+        scratch[grp * MROWS + row] = sv;
         __syncthreads();
         if (tid < MROWS) {
             float t = 0.f;
@@ -406,87 +466,101 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
 
     if (EPI == EPI_QKV) {
         // Tile = one head of Q, K or V (all three regions are multiples of 128).
-        const uint32_t base = tile * BN;
+        const uint32_t base = tile * TBN;
         const uint32_t i = tid & 63;                       // rotation pair (2i, 2i+1)
-        const float omega = powf(p.rope_base, -2.0f * (float)i / (float)DH);
-        float sn, cs;
-        sincosf((float)p.cache_len * omega, &sn, &cs);
+        const float cs = rope_cs, sn = rope_sn;
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
             const uint32_t b = 4 * (tid >> 6) + rr;
             if (b >= p.batch) continue;
             const float r1 = rsqrtf(red_ss[b] / (float)p.d + p.eps);
-            const float v0 = red[b * BN + 2 * i] * r1, v1 = red[b * BN + 2 * i + 1] * r1;
+            const float2 vv = *reinterpret_cast<const float2*>(&red[b * TBN + 2 * i]);
+            const float v0 = vv.x * r1, v1 = vv.y * r1;
             if (base < p.d) {
                 // pre-scaled by 1/sqrt(Dh) and rounded once for the q.k^T MFMA
                 const float qs = rsqrtf((float)DH);
-                uint16_t* qd = p.q + (size_t)b * p.d + base + 2 * i;
-                qd[0] = f2bf((v0 * cs - v1 * sn) * qs);
-                qd[1] = f2bf((v0 * sn + v1 * cs) * qs);
+                *reinterpret_cast<uint32_t*>(p.q + (size_t)b * p.d + base + 2 * i) =
+                    pack_bf16((v0 * cs - v1 * sn) * qs, (v0 * sn + v1 * cs) * qs);
             } else if (base < p.d + p.hkv * DH) {
                 const uint32_t kvh = (base - p.d) / DH;
-                uint16_t* kd = p.k_new + ((size_t)b * p.hkv + kvh) * DH + 2 * i;
-                kd[0] = f2bf(v0 * cs - v1 * sn);
-                kd[1] = f2bf(v0 * sn + v1 * cs);
+                *reinterpret_cast<uint32_t*>(p.k_new + ((size_t)b * p.hkv + kvh) * DH + 2 * i) =
+                    pack_bf16(v0 * cs - v1 * sn, v0 * sn + v1 * cs);
             } else {
                 const uint32_t kvh = (base - p.d - p.hkv * DH) / DH;
-                uint16_t* vd = p.v_new + ((size_t)b * p.hkv + kvh) * DH + 2 * i;
-                vd[0] = f2bf(v0);
-                vd[1] = f2bf(v1);
+                *reinterpret_cast<uint32_t*>(p.v_new + ((size_t)b * p.hkv + kvh) * DH + 2 * i) =
+                    pack_bf16(v0, v1);
             }
         }
     } else if (EPI == EPI_WO) {
-        // thread: row eb, columns ec .. ec+7; x1 = x + attn W_o
-        float v[8];
+        // thread: row eb, columns ec .. ec+7; x1 = x + attn W_o (rows past
+        // the batch computed from x row 0, never stored, their sums zeroed)
+        const f32x4 r0 = *reinterpret_cast<const f32x4*>(&red[eb * TBN + ec]);
+        const f32x4 r1 = *reinterpret_cast<const f32x4*>(&red[eb * TBN + ec + 4]);
+        float xv[8];
         float sq = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const uint32_t xb = pre_x[e / 2] >> (16 * (e & 1));
-            v[e] = eb < p.batch ? bf2f((uint16_t)xb) + red[eb * BN + ec + e] : 0.f;
-            sq += v[e] * v[e];
+            const uint32_t xw = pre_x[e / 2];
+            xv[e] = __uint_as_float((e & 1) ? (xw & 0xffff0000u) : (xw << 16)) +
+                    (e < 4 ? r0[e] : r1[e - 4]);
+            sq += xv[e] * xv[e];
         }
         if (eb < p.batch) {
-            const size_t o = (size_t)eb * p.d + tile * BN + ec;
-            *reinterpret_cast<f32x4*>(p.x1 + o) = f32x4{v[0], v[1], v[2], v[3]};
-            *reinterpret_cast<f32x4*>(p.x1 + o + 4) = f32x4{v[4], v[5], v[6], v[7]};
-            u32x4 hi, lo;
+            const size_t o = (size_t)eb * p.d + tile * TBN + ec;
+            *reinterpret_cast<f32x4*>(p.x1 + o) = f32x4{xv[0], xv[1], xv[2], xv[3]};
+            *reinterpret_cast<f32x4*>(p.x1 + o + 4) = f32x4{xv[4], xv[5], xv[6], xv[7]};
+            uint32_t hi[4], lo[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint16_t h0 = f2bf(v[2 * e]), h1 = f2bf(v[2 * e + 1]);
-                hi[e] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-                lo[e] = (uint32_t)f2bf(v[2 * e] - bf2f(h0)) |
-                        ((uint32_t)f2bf(v[2 * e + 1] - bf2f(h1)) << 16);
-            }
-            *reinterpret_cast<u32x4*>(p.x1b + o) = hi;
-            *reinterpret_cast<u32x4*>(p.x1b_lo + o) = lo;
+            for (int e = 0; e < 4; ++e) split_bf16(xv[2 * e], xv[2 * e + 1], hi[e], lo[e]);
+            *reinterpret_cast<u32x4*>(p.x1b + o) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+            *reinterpret_cast<u32x4*>(p.x1b_lo + o) = u32x4{lo[0], lo[1], lo[2], lo[3]};
         }
         // row sums of x1^2 over the tile: the 16 threads of a row are 16 adjacent lanes
 #pragma unroll
         for (int o2 = 8; o2 > 0; o2 >>= 1) sq += __shfl_xor(sq, o2);
-        if ((tid & 15) == 0) p.sumsq2[tile * MROWS + eb] = sq;
+        if ((tid & 15) == 0) p.sumsq2[tile * MROWS + eb] = eb < p.batch ? sq : 0.f;
     } else if (EPI == EPI_GU) {
-#pragma unroll
-        for (int i = 0; i < (MROWS * 64) / 256; ++i) {
-            const uint32_t idx = tid + 256 * i, b = idx / 64, c = idx % 64;
-            if (b >= p.batch) continue;
+        // tile = gate columns [TBN/2 tile, +TBN/2) and the matching up columns;
+        // thread: row tid / 16, CPT consecutive columns (vector LDS reads and
+        // stores, no per-element branch)
+        constexpr int HALF = TBN / 2, CPT = HALF / 16;
+        const uint32_t b = tid >> 4, c0 = CPT * (tid & 15);
+        if (b < p.batch) {
             const float r2 = red_ss[b];
-            const float gate = red[b * BN + c] * r2, up = red[b * BN + 64 + c] * r2;
-            const float av = silu(gate) * up;
-            const uint16_t hi = f2bf(av);
-            const size_t o = (size_t)b * p.ff + tile * 64 + c;
-            p.act[o] = hi;
-            p.act_lo[o] = f2bf(av - bf2f(hi));
+            uint32_t hi[CPT / 2], lo[CPT / 2];
+#pragma unroll
+            for (int q = 0; q < CPT / 4; ++q) {
+                const f32x4 gv = *reinterpret_cast<const f32x4*>(&red[b * TBN + c0 + 4 * q]);
+                const f32x4 uv = *reinterpret_cast<const f32x4*>(&red[b * TBN + HALF + c0 + 4 * q]);
+#pragma unroll
+                for (int e = 0; e < 4; e += 2) {
+                    const float a0 = silu(gv[e] * r2) * (uv[e] * r2);
+                    const float a1 = silu(gv[e + 1] * r2) * (uv[e + 1] * r2);
+                    split_bf16(a0, a1, hi[2 * q + e / 2], lo[2 * q + e / 2]);
+                }
+            }
+            const size_t o = (size_t)b * p.ff + tile * HALF + c0;
+#pragma unroll
+            for (int q = 0; q < CPT / 8; ++q) {
+                *reinterpret_cast<u32x4*>(p.act + o + 8 * q) =
+                    u32x4{hi[4 * q], hi[4 * q + 1], hi[4 * q + 2], hi[4 * q + 3]};
+                *reinterpret_cast<u32x4*>(p.act_lo + o + 8 * q) =
+                    u32x4{lo[4 * q], lo[4 * q + 1], lo[4 * q + 2], lo[4 * q + 3]};
+            }
+            if (CPT == 4) {
+                *reinterpret_cast<uint2*>(p.act + o) = uint2{hi[0], hi[1]};
+                *reinterpret_cast<uint2*>(p.act_lo + o) = uint2{lo[0], lo[1]};
+            }
         }
     } else {   // EPI_DOWN: y = x1 + act W_down; thread: row eb, columns ec .. ec+7
+        const f32x4 r0 = *reinterpret_cast<const f32x4*>(&red[eb * TBN + ec]);
+        const f32x4 r1 = *reinterpret_cast<const f32x4*>(&red[eb * TBN + ec + 4]);
         if (eb < p.batch) {
-            u32x4 out;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float y0 = pre_x1[e / 2][2 * (e & 1)] + red[eb * BN + ec + 2 * e];
-                const float y1 = pre_x1[e / 2][2 * (e & 1) + 1] + red[eb * BN + ec + 2 * e + 1];
-                out[e] = (uint32_t)f2bf(y0) | ((uint32_t)f2bf(y1) << 16);
-            }
-            *reinterpret_cast<u32x4*>(p.y + (size_t)eb * p.d + tile * BN + ec) = out;
+            const u32x4 out = {pack_bf16(pre_x1[0][0] + r0[0], pre_x1[0][1] + r0[1]),
+                               pack_bf16(pre_x1[0][2] + r0[2], pre_x1[0][3] + r0[3]),
+                               pack_bf16(pre_x1[1][0] + r1[0], pre_x1[1][1] + r1[1]),
+                               pack_bf16(pre_x1[1][2] + r1[2], pre_x1[1][3] + r1[3])};
+            *reinterpret_cast<u32x4*>(p.y + (size_t)eb * p.d + tile * TBN + ec) = out;
         }
     }
     reset_counter(&g.counters[tile]);   // ready for the next step
@@ -519,15 +593,7 @@ constexpr int AKEYS = 64;                 // keys per workgroup iteration
 constexpr int APITCH = DH + 4;            // floats per (split, head) partial: o[DH], m, l, pad
 constexpr int QP = DH + 8;                // LDS pitch (bf16) of a query row
 constexpr float NEG_BIG = -1.0e30f;       // "no key yet": finite, so max/exp never see inf - inf
-constexpr float LOG2E = 1.4426950408889634f;
 constexpr uint32_t ATTN_WGS = 1024;      // attention grid target: 4 workgroups per CU
-
-__device__ __forceinline__ void* uniform_ptr(const void* ptr) {
-    const uint64_t v = reinterpret_cast<uint64_t>(ptr);
-    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return reinterpret_cast<void*>((hi << 32) | lo);
-}
 
 struct KVBlock {
     u32x4 k[4];      // K[key j][32 m + 8 grp .. + 8] for the scores MFMA, m < 4
@@ -751,8 +817,8 @@ void attention_kernel(StepParams p) {
                           __uint_as_float(vv.y << 16), __uint_as_float(vv.y & 0xffff0000u)};
         const f32x4 res = (O * so + wn * vn) / (L * so + wn);
         uint2 out;
-        out.x = (uint32_t)f2bf(res[0]) | ((uint32_t)f2bf(res[1]) << 16);
-        out.y = (uint32_t)f2bf(res[2]) | ((uint32_t)f2bf(res[3]) << 16);
+        out.x = pack_bf16(res[0], res[1]);
+        out.y = pack_bf16(res[2], res[3]);
         *reinterpret_cast<uint2*>(p.attn_out + (size_t)b * p.d + (kvh * G + h) * DH + 4 * d4) = out;
     }
     reset_counter(&p.attn_counters[bk]);
@@ -762,16 +828,25 @@ void attention_kernel(StepParams p) {
 
 struct Plan {
     uint32_t nqkv, g, nsplit, split_keys;
-    uint32_t tiles[4], splits[4];
+    uint32_t tiles[4], splits[4], kc[4], ring[4], ww[4];
     size_t off_counters, off_partial, off_sumsq, off_q, off_attn_part, off_attn_out, off_x1,
         off_x1b, off_x1b_lo, off_sumsq2, off_act, off_act_lo, total;
     uint32_t counter_base[5];   // qkv, attn, wo, gu, down
 };
 
-// Steps per K split: 4 (128 KB of weights in flight per workgroup) when the
-// K range divides, else 2 or 1.
-static uint32_t choose_steps(uint32_t ksteps) {
-    return ksteps % 4 == 0 ? 4u : (ksteps % 2 == 0 ? 2u : 1u);
+// K split of a skinny GEMM: enough splits that tiles x splits gives about one
+// workgroup per CU (fewer, longer streams read HBM faster than two per CU),
+// each split a whole number of 128-row steps; the ring holds RING units of
+// 128 / ww rows, or the split's unit count below that.
+static void choose_split(uint32_t tiles, uint32_t ksteps, uint32_t ww, uint32_t* splits,
+                         uint32_t* kc, uint32_t* ring) {
+    const uint32_t slots = std::max(device_cu_count(), 1u);
+    const uint32_t want = std::min(std::max(1u, slots / tiles), ksteps);
+    const uint32_t per = cdiv(ksteps, want);
+    *splits = cdiv(ksteps, per);
+    *kc = per * KS;
+    const uint32_t units = per * ww;
+    *ring = units >= RING ? RING : (units >= 2 ? 2 : 1);
 }
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -814,15 +889,25 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
     }
     pl->tiles[EPI_QKV] = pl->nqkv / BN;
     pl->tiles[EPI_WO] = D / BN;
-    pl->tiles[EPI_GU] = FF / 64;
+    // W_gate | W_up in 512-column tiles (1 KB row segments) when d_ff allows
+    pl->ww[EPI_QKV] = pl->ww[EPI_WO] = pl->ww[EPI_DOWN] = 1;
+    pl->ww[EPI_GU] = FF % (2 * BN) == 0 ? 4 : 1;
+    pl->tiles[EPI_GU] = FF / (BN / 2 * pl->ww[EPI_GU]);
     pl->tiles[EPI_DOWN] = D / BN;
-    pl->splits[EPI_QKV] = (D / KS) / choose_steps(D / KS);
-    pl->splits[EPI_WO] = (D / KS) / choose_steps(D / KS);
-    pl->splits[EPI_GU] = (D / KS) / choose_steps(D / KS);
-    pl->splits[EPI_DOWN] = (FF / KS) / choose_steps(FF / KS);
+    const uint32_t ldw[4] = {pl->nqkv, D, 2 * FF, D};
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t k = i == EPI_DOWN ? FF : D;
+        choose_split(pl->tiles[i], k / KS, pl->ww[i], &pl->splits[i], &pl->kc[i], &pl->ring[i]);
+        // the ring's clipped loads run up to RING units past the split
+        const uint64_t unit = KS / pl->ww[i];
+        const uint64_t trips = cdiv(pl->kc[i] / (uint32_t)unit, pl->ring[i]);
+        if ((trips + 1) * pl->ring[i] * unit * ldw[i] * 2 > 0xffffffffull ||
+            (uint64_t)B * k * 2 >= 0x80000000ull)
+            return fail(MB_E_ARG, "decoder step: shapes too large for 32-bit weight offsets");
+    }
     size_t max_part = 0;
     for (int i = 0; i < 4; ++i)
-        max_part = std::max(max_part, (size_t)pl->tiles[i] * pl->splits[i]);
+        max_part = std::max(max_part, (size_t)pl->tiles[i] * pl->splits[i] * pl->ww[i]);
     const uint32_t n_counters = pl->tiles[EPI_QKV] + B * a->n_kv_heads + pl->tiles[EPI_WO] +
                                 pl->tiles[EPI_GU] + pl->tiles[EPI_DOWN];
     pl->counter_base[0] = 0;
@@ -855,14 +940,22 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
 // it is read within a step.
 static size_t counters_bytes(const Plan& pl) { return pl.off_partial; }
 
-template <int EPI>
-void launch_skinny(const GemmCfg& g, const StepParams& p, hipStream_t s) {
+template <int EPI, int WW>
+void launch_skinny_ww(const GemmCfg& g, uint32_t ring, const StepParams& p, hipStream_t s) {
     const dim3 grid(g.tiles * g.splits), block(256);
-    switch (g.kc / KS) {
-        case 1: hipLaunchKernelGGL((skinny_gemm_kernel<EPI, 1>), grid, block, 0, s, g, p); break;
-        case 2: hipLaunchKernelGGL((skinny_gemm_kernel<EPI, 2>), grid, block, 0, s, g, p); break;
-        default: hipLaunchKernelGGL((skinny_gemm_kernel<EPI, 4>), grid, block, 0, s, g, p); break;
+    switch (ring) {
+        case 1: hipLaunchKernelGGL((skinny_gemm_kernel<EPI, WW, 1>), grid, block, 0, s, g, p); break;
+        case 2: hipLaunchKernelGGL((skinny_gemm_kernel<EPI, WW, 2>), grid, block, 0, s, g, p); break;
+        default: hipLaunchKernelGGL((skinny_gemm_kernel<EPI, WW, RING>), grid, block, 0, s, g, p); break;
     }
+}
+
+template <int EPI>
+void launch_skinny(const GemmCfg& g, const Plan& pl, const StepParams& p, hipStream_t s) {
+    if constexpr (EPI == EPI_GU) {
+        if (pl.ww[EPI] == 4) return launch_skinny_ww<EPI, 4>(g, pl.ring[EPI], p, s);
+    }
+    launch_skinny_ww<EPI, 1>(g, pl.ring[EPI], p, s);
 }
 
 int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) {
@@ -916,7 +1009,7 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
                     const uint16_t* w, uint32_t ldw, uint32_t k, uint32_t counter_base) -> GemmCfg {
         GemmCfg g;
         g.a = act; g.a_lo = act_lo; g.lda = lda; g.w = w; g.ldw = ldw; g.k = k;
-        g.tiles = pl.tiles[epi]; g.splits = pl.splits[epi]; g.kc = k / g.splits;
+        g.tiles = pl.tiles[epi]; g.splits = pl.splits[epi]; g.kc = pl.kc[epi];
         g.paired = epi == EPI_GU ? 1u : 0u;
         g.counters = counters + counter_base;
         return g;
@@ -932,7 +1025,7 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
 
     auto mark = [&](const char* name) { if (pm) pm->mark(s, name); };
     mark("qkv_rope");
-    launch_skinny<EPI_QKV>(g_qkv, p, s);
+    launch_skinny<EPI_QKV>(g_qkv, pl, p, s);
     MB_LAUNCH_CHECK("decoder qkv_rope");
     mark("attention");
     {
@@ -943,13 +1036,13 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
     }
     MB_LAUNCH_CHECK("decoder attention");
     mark("wo_residual");
-    launch_skinny<EPI_WO>(g_wo, p, s);
+    launch_skinny<EPI_WO>(g_wo, pl, p, s);
     MB_LAUNCH_CHECK("decoder wo_residual");
     mark("gate_up_swiglu");
-    launch_skinny<EPI_GU>(g_gu, p, s);
+    launch_skinny<EPI_GU>(g_gu, pl, p, s);
     MB_LAUNCH_CHECK("decoder gate_up_swiglu");
     mark("down_residual");
-    launch_skinny<EPI_DOWN>(g_dn, p, s);
+    launch_skinny<EPI_DOWN>(g_dn, pl, p, s);
     MB_LAUNCH_CHECK("decoder down_residual");
     return MB_OK;
 }
@@ -999,7 +1092,7 @@ int run_decoder(const Bindings& bs, hipStream_t s, PartMarks* pm) {
 
 void register_decoder() {
     register_kernel({"llama_decoder_step_bf16", run_decoder,
-                     reinterpret_cast<const void*>(&skinny_gemm_kernel<EPI_GU, 4>), 5});
+                     reinterpret_cast<const void*>(&skinny_gemm_kernel<EPI_GU, 4, RING>), 5});
 }
 
 }  // namespace mb

@@ -74,10 +74,10 @@ def _check(got, want, what):
 
 @pytest.mark.parametrize("B,D,H,HKV,FF,L", [
     (2, 512, 4, 2, 1024, 40),      # smoke shape
-    (1, 256, 2, 1, 384, 0),        # empty cache: attends to itself only
-    (2, 512, 4, 2, 512, 0),        # empty cache, 512-row K splits
+    (1, 256, 2, 1, 384, 0),        # empty cache: attends to itself only; 128-col gate|up tiles
+    (2, 512, 4, 2, 512, 0),        # empty cache
     (3, 512, 4, 4, 256, 5),        # MHA (G = 1)
-    (4, 512, 4, 4, 512, 5),        # MHA (G = 1), 512-row K splits
+    (4, 512, 4, 4, 512, 5),        # MHA (G = 1)
     (16, 1024, 8, 1, 512, 128),    # G = 8, one full 128-key split + the new key
     (5, 512, 4, 2, 640, 129),      # split boundary + 1
     (7, 1024, 8, 2, 1024, 300),    # several 64-key blocks, ragged
