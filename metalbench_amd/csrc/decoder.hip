@@ -593,7 +593,6 @@ constexpr int AKEYS = 64;                 // keys per workgroup iteration
 constexpr int APITCH = DH + 4;            // floats per (split, head) partial: o[DH], m, l, pad
 constexpr int QP = DH + 8;                // LDS pitch (bf16) of a query row
 constexpr float NEG_BIG = -1.0e30f;       // "no key yet": finite, so max/exp never see inf - inf
-constexpr uint32_t ATTN_WGS = 1024;      // attention grid target: 4 workgroups per CU
 
 struct KVBlock {
     u32x4 k[4];      // K[key j][32 m + 8 grp .. + 8] for the scores MFMA, m < 4
@@ -766,34 +765,51 @@ void attention_kernel(StepParams p) {
     if (!arrive_last(&p.attn_counters[bk], p.nsplit, &s_last)) return;
 
     // ---- merge: the splits' partials plus the new token ----
-    for (uint32_t h = wave; h < G; h += 4) {       // s_new = q . k_new (q is pre-scaled)
-        const uint32_t qa = *reinterpret_cast<const uint32_t*>(
-            p.q + (size_t)b * p.d + (kvh * G + h) * DH + 2 * lane);
-        const uint32_t ka = *reinterpret_cast<const uint32_t*>(knew + 2 * lane);
-        float d = __uint_as_float(qa << 16) * __uint_as_float(ka << 16) +
-                  __uint_as_float(qa & 0xffff0000u) * __uint_as_float(ka & 0xffff0000u);
-#pragma unroll
-        for (int o2 = 32; o2 > 0; o2 >>= 1) d += __shfl_xor(d, o2);
-        if (lane == 0) s_new[h] = d;
-    }
-    __syncthreads();
+    // One memory round trip in the common case: the first U splits' partials
+    // of this thread's first item (head h, d quad d4) and the new value are
+    // loaded together with the q rows and the new key of the q . k_new scores.
     constexpr uint32_t U = 8;                      // splits per batch of loads
     const uint32_t parts = bk * p.nsplit * G * APITCH * 4;
-    for (uint32_t idx = tid; idx < G * (DH / 4); idx += 256) {
+    const uint32_t nitems = G * (DH / 4);
+    f32x4 oc[U];
+    float mc[U], lc[U];
+    auto load_batch = [&](uint32_t idx, uint32_t c0) {
         const uint32_t h = idx / (DH / 4), d4 = idx % (DH / 4);
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {     // past the last split: reload it, weight 0
+            const uint32_t c = min(c0 + u, p.nsplit - 1);
+            const uint32_t at = parts + (c * G + h) * APITCH * 4;
+            oc[u] = ld4_sc1(ars, at + 16 * d4);
+            mc[u] = ld_sc1(ars, at + DH * 4);
+            lc[u] = ld_sc1(ars, at + (DH + 1) * 4);
+        }
+    };
+    load_batch(min(tid, nitems - 1), 0);
+    const uint2 vv0 = *reinterpret_cast<const uint2*>(vnew + 4 * (tid % (DH / 4)));
+    {   // s_new = q . k_new (q is pre-scaled); wave w takes heads w, w + 4, ...
+        const uint32_t ka = *reinterpret_cast<const uint32_t*>(knew + 2 * lane);
+        uint32_t qa[GT / 4];
+#pragma unroll
+        for (int i = 0; i < GT / 4; ++i)
+            qa[i] = *reinterpret_cast<const uint32_t*>(
+                p.q + (size_t)b * p.d + (kvh * G + min(wave + 4 * i, G - 1)) * DH + 2 * lane);
+#pragma unroll
+        for (int i = 0; i < GT / 4; ++i) {
+            float d = __uint_as_float(qa[i] << 16) * __uint_as_float(ka << 16) +
+                      __uint_as_float(qa[i] & 0xffff0000u) * __uint_as_float(ka & 0xffff0000u);
+#pragma unroll
+            for (int o2 = 32; o2 > 0; o2 >>= 1) d += __shfl_xor(d, o2);
+            if (lane == 0 && wave + 4 * i < G) s_new[wave + 4 * i] = d;
+        }
+    }
+    __syncthreads();
+    for (uint32_t idx = tid; idx < nitems; idx += 256) {
+        const uint32_t h = idx / (DH / 4), d4 = idx % (DH / 4);
+        if (idx != tid) load_batch(idx, 0);        // a second item per thread (G > 8)
         float M = NEG_BIG, L = 0.f;
         f32x4 O = {};
         for (uint32_t c0 = 0; c0 < p.nsplit; c0 += U) {
-            f32x4 oc[U];
-            float mc[U], lc[U];
-#pragma unroll
-            for (uint32_t u = 0; u < U; ++u) {     // past the last split: reload it, weight 0
-                const uint32_t c = min(c0 + u, p.nsplit - 1);
-                const uint32_t at = parts + (c * G + h) * APITCH * 4;
-                oc[u] = ld4_sc1(ars, at + 16 * d4);
-                mc[u] = ld_sc1(ars, at + DH * 4);
-                lc[u] = ld_sc1(ars, at + (DH + 1) * 4);
-            }
+            if (c0 > 0) load_batch(idx, c0);
             float Mb = M;
 #pragma unroll
             for (uint32_t u = 0; u < U; ++u) Mb = fmaxf(Mb, mc[u]);
@@ -812,7 +828,7 @@ void attention_kernel(StepParams p) {
         const float Mf = fmaxf(M, sn);
         const float so = __builtin_amdgcn_exp2f((M - Mf) * LOG2E);
         const float wn = __builtin_amdgcn_exp2f((sn - Mf) * LOG2E);
-        const uint2 vv = *reinterpret_cast<const uint2*>(vnew + 4 * d4);
+        const uint2 vv = idx == tid ? vv0 : *reinterpret_cast<const uint2*>(vnew + 4 * d4);
         const f32x4 vn = {__uint_as_float(vv.x << 16), __uint_as_float(vv.x & 0xffff0000u),
                           __uint_as_float(vv.y << 16), __uint_as_float(vv.y & 0xffff0000u)};
         const f32x4 res = (O * so + wn * vn) / (L * so + wn);
@@ -876,10 +892,11 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
     const uint32_t D = a->d_model, FF = a->d_ff, B = a->batch;
     pl->nqkv = D + 2 * a->n_kv_heads * DH;
     pl->g = a->n_heads / a->n_kv_heads;
-    {   // attention: ~ATTN_WGS workgroups; splits of a multiple of 128 keys (an even
+    {   // attention: about one workgroup per CU (fewer, longer streams read HBM
+        // faster than several per CU); splits of a multiple of 128 keys (an even
         // number of 64-key iterations, as the loop is unrolled by two)
         const uint32_t pairs = B * a->n_kv_heads;
-        const uint32_t want = std::max(1u, cdiv(ATTN_WGS, pairs));
+        const uint32_t want = std::max(1u, cdiv(std::max(device_cu_count(), 1u), pairs));
         const uint32_t nmax = std::max(1u, cdiv(a->cache_len, 2 * AKEYS));
         const uint32_t per = cdiv(std::max(a->cache_len, 1u), std::min(want, nmax));
         pl->split_keys = cdiv(per, 2 * AKEYS) * 2 * AKEYS;
