@@ -81,21 +81,33 @@ void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt
         row_base[i] = (uint64_t)nn * sh.h * sh.w * sh.c;
     }
 
-    float4 ra[LOADS], rb[LOADS];
-    auto load = [&](uint32_t k0) {
+    // Two register stages (see the stage loop below).  FAST loads are buffer
+    // loads: taps outside the image and k past the filter read zeros through
+    // an out-of-range offset, so the loads carry no branches.
+    float4 ra[2][LOADS], rb[2][LOADS];
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(X), 0, sh.n * sh.h * sh.w * sh.c * 4, 0x00020000u);
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(Wt), 0, sh.o * sh.k * 4, 0x00020000u);
+    auto ld4 = [](__amdgpu_buffer_rsrc_t rsrc, uint32_t off) {
+        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
+    };
+    auto load = [&](int set, uint32_t k0) {
         if (FAST) {
-            // Uniform tap for the stage: k0 = (r*S + s)*C + c0.
+            // Uniform tap for the stage: k0 = (r*S + s)*C + c0 (k0 past the filter
+            // gives r >= R, which the row test below turns into zeros).
             const uint32_t rs = k0 / sh.c, c0 = k0 - rs * sh.c;
             const uint32_t r = rs / sh.s, s = rs - r * sh.s;
 #pragma unroll
             for (int i = 0; i < LOADS; ++i) {
                 const uint32_t q4 = ((tid + i * NT) & 7) * 4;
                 const int32_t hi = row_h0[i] + (int32_t)r, wi = row_w0[i] + (int32_t)s;
-                const bool in = row_ok[i] && hi >= 0 && hi < (int32_t)sh.h && wi >= 0 &&
-                                wi < (int32_t)sh.w;
-                ra[i] = in ? *reinterpret_cast<const float4*>(
-                                 X + row_base[i] + ((uint64_t)hi * sh.w + wi) * sh.c + c0 + q4)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
+                const bool in = row_ok[i] && k0 < sh.k && hi >= 0 && hi < (int32_t)sh.h &&
+                                wi >= 0 && wi < (int32_t)sh.w;
+                const uint32_t off =
+                    in ? ((uint32_t)row_base[i] + ((uint32_t)hi * sh.w + wi) * sh.c + c0 + q4) * 4
+                       : 0x80000000u;
+                ra[set][i] = ld4(xrs, off);
             }
         } else {
 #pragma unroll
@@ -114,7 +126,7 @@ void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt
                             v[e] = X[row_base[i] + ((uint64_t)hi * sh.w + wi) * sh.c + c];
                     }
                 }
-                ra[i] = make_float4(v[0], v[1], v[2], v[3]);
+                ra[set][i] = make_float4(v[0], v[1], v[2], v[3]);
             }
         }
         // B tile: 64 output channels x 32 k, rows of w are K-contiguous.
@@ -123,51 +135,71 @@ void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt
             const uint32_t q = tid + i * NT;
             const uint32_t oc = n0 + (q >> 3), kq = k0 + (q & 7) * 4;
             if (FAST) {
-                rb[i] = (oc < sh.o && kq < sh.k)
-                            ? *reinterpret_cast<const float4*>(Wt + (uint64_t)oc * sh.k + kq)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
+                rb[set][i] = ld4(wrs, (oc < sh.o && kq < sh.k) ? (oc * sh.k + kq) * 4 : 0x80000000u);
             } else {
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     v[e] = (oc < sh.o && kq + e < sh.k) ? Wt[(uint64_t)oc * sh.k + kq + e] : 0.f;
-                rb[i] = make_float4(v[0], v[1], v[2], v[3]);
+                rb[set][i] = make_float4(v[0], v[1], v[2], v[3]);
             }
         }
     };
-    auto store = [&](int buf) {
+    auto store = [&](int set, int buf) {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             const uint32_t q = tid + i * NT;
-            *reinterpret_cast<float4*>(&As[buf][(q >> 3) * SK + (q & 7) * 4]) = ra[i];
-            *reinterpret_cast<float4*>(&Bs[buf][(q >> 3) * SK + (q & 7) * 4]) = rb[i];
+            *reinterpret_cast<float4*>(&As[buf][(q >> 3) * SK + (q & 7) * 4]) = ra[set][i];
+            *reinterpret_cast<float4*>(&Bs[buf][(q >> 3) * SK + (q & 7) * 4]) = rb[set][i];
         }
     };
 
     f32x16 acc = {};
     const uint32_t li = lane & 31, lh = lane >> 5;
+    // FAST: an even number of stages and no branch in the loop body (a stage
+    // past K multiplies the zeros its out-of-range loads stored).
+    const uint32_t nrun = FAST ? (nstages + 1) & ~1u : nstages;
     if (nstages > 0) {
-        load(0);
-        store(0);
+        load(0, 0);
+        if (FAST || nstages > 1) load(1, BK);
+        store(0, 0);
         __syncthreads();
     }
-    for (uint32_t st = 0; st < nstages; ++st) {
-        const int cur = st & 1;
-        if (st + 1 < nstages) load((st + 1) * BK);
+    // Stage st: the loads of stage st+2 go into the register set stored at
+    // the end of stage st-1 and stay in flight for two stages; stage st+1's
+    // registers go to LDS in the middle of stage st's MFMAs.  The operands of
+    // group g+1 are read from LDS while group g's MFMAs run.
+    auto stage = [&](uint32_t st, int cur) {
+        if (FAST || st + 2 < nstages) load(cur, (st + 2) * BK);
+        __builtin_amdgcn_sched_barrier(0);
         const float* as = &As[cur][(wm * 32 + li) * SK + 4 * lh];
         const float* bs = &Bs[cur][(wn * 32 + li) * SK + 4 * lh];
+        constexpr int NG = BK / 8 / KSPLIT;
+        float4 a4[2], b4[2];
+        auto read_ops = [&](int gg, int slot) {
+            const int g = (int)wk * NG + gg;
+            a4[slot] = *reinterpret_cast<const float4*>(as + 8 * g);
+            b4[slot] = *reinterpret_cast<const float4*>(bs + 8 * g);
+        };
+        read_ops(0, 0);
 #pragma unroll
-        for (int gg = 0; gg < 4 / KSPLIT; ++gg) {
-            const int g = (int)wk * (4 / KSPLIT) + gg;
-            const float4 a4 = *reinterpret_cast<const float4*>(as + 8 * g);
-            const float4 b4 = *reinterpret_cast<const float4*>(bs + 8 * g);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.x, b4.x, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.y, b4.y, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.z, b4.z, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.w, b4.w, acc, 0, 0, 0);
+        for (int gg = 0; gg < NG; ++gg) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (gg + 1 < NG) read_ops(gg + 1, (gg + 1) & 1);
+            if (gg == NG / 2 && (FAST || st + 1 < nstages)) store(cur ^ 1, cur ^ 1);
+            __builtin_amdgcn_sched_barrier(0);
+            const int sl = gg & 1;
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[sl].x, b4[sl].x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[sl].y, b4[sl].y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[sl].z, b4[sl].z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[sl].w, b4[sl].w, acc, 0, 0, 0);
         }
-        if (st + 1 < nstages) store(cur ^ 1);
+        __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
+    };
+    for (uint32_t st = 0; st < nrun; st += 2) {
+        stage(st, 0);
+        if (FAST || st + 1 < nstages) stage(st + 1, 1);
     }
 
     if (KSPLIT == 2) {
@@ -214,7 +246,11 @@ int launch_conv2d(const float* x, const float* w, float* y, uint32_t n, uint32_t
     const uint32_t tiles_m = cdiv(sh.m, BM), tiles_n = cdiv(o, BN);
     const uint64_t nblocks = (uint64_t)tiles_m * tiles_n;
     if (nblocks > 0x7fffffffull) return fail(MB_E_ARG, "conv2d_f32: shape too large");
-    const bool fast = (c % BK == 0) && ((((uintptr_t)x) | ((uintptr_t)w)) & 15) == 0;
+    // FAST: a stage never straddles a tap, 16-byte aligned rows, and buffer-load
+    // offsets of both operands within 2 GB
+    const bool fast = (c % BK == 0) && ((((uintptr_t)x) | ((uintptr_t)w)) & 15) == 0 &&
+                      (uint64_t)n * h * wd * c * 4 < 0x80000000ull &&
+                      (uint64_t)o * k * 4 < 0x80000000ull;
     if (fast)
         hipLaunchKernelGGL((conv2d_f32_kernel<2, true>), dim3((uint32_t)nblocks), dim3(512), 0, st,
                            x, w, y, sh, tiles_n);

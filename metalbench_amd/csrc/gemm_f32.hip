@@ -20,8 +20,10 @@
 // gfx950 design.  fp32 MFMA peak is 256 flop/clk/CU (157.3 TFLOP/s), so at
 // 1024^3 the whole problem is ~32k MFMA cycles per CU: the kernel must keep one
 // 64x64 tile per CU busy from its first cycle.
-//  * workgroup tile 64x64, BK = 32 per stage, LDS double buffered, one barrier
-//    per stage; global loads of stage s+1 are in flight during the MFMAs of s;
+//  * workgroup tile 64x64, BK = 64 per stage, LDS double buffered, one barrier
+//    per stage; operands are register-staged two stages ahead: the global loads
+//    of stage s+2 are in flight during the MFMAs of stage s (one stage is
+//    ~1000 MFMA cycles, shorter than a loaded L2 round trip);
 //  * 4 waves own a 2x2 grid of 32x32 sub-tiles (v_mfma_f32_32x32x2f32);
 //    KSPLIT=2 adds a second set of 4 waves that takes the other half of each
 //    stage's K range (two waves per SIMD to hide LDS/MFMA latency) and the two
@@ -44,7 +46,8 @@ namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 64, BN = 64, BK = 32;
+constexpr int BM = 64, BN = 64, BK = 64;
+constexpr int KQ = BK / 4;     // float4s per K-contiguous row of a stage
 constexpr int SA = BK + 4;   // As (and transposed Bs) row stride (floats)
 constexpr int SB = BN + 4;   // Bs row stride (floats)
 
@@ -57,7 +60,7 @@ template <int KSPLIT, bool VEC, int BL, int EPI, bool RMS>
 __global__ __launch_bounds__(256 * KSPLIT)
 void gemm_f32_kernel(GemmF32Args g) {
     constexpr int NT = 256 * KSPLIT;
-    constexpr int LOADS = 512 / NT;   // float4 per thread per operand per stage
+    constexpr int LOADS = BM * KQ / NT;   // float4 per thread per operand per stage
     constexpr bool DUAL = EPI == EPI_SWIGLU;
     constexpr int NB = DUAL ? 2 : 1;
     constexpr int BSZ = BL == BL_KN ? BK * SB : BN * SA;
@@ -81,49 +84,67 @@ void gemm_f32_kernel(GemmF32Args g) {
                           DUAL ? g.b2 + (size_t)blockIdx.y * g.batch_b : nullptr};
     float* C = g.c + (size_t)blockIdx.y * g.batch_c;
 
-    float4 ra[LOADS], rb[NB][LOADS];
+    // two register stages: the loads of stage s+2 go out while stage s is
+    // multiplied and stage s+1 (loaded during stage s-1) goes to LDS
+    float4 ra[2][LOADS], rb[2][NB][LOADS];
     float ss[LOADS] = {};   // RMS: this thread's sum of squares of its A row
 
+    // VEC: buffer loads, out-of-range float4s read as zeros through an
+    // out-of-range offset (no branch, so the waitcnt pass sees one fixed load
+    // order; the host keeps every operand under 2 GB)
+    const uint32_t a_bytes = M * g.lda * 4;
+    const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(A), 0, a_bytes, 0x00020000u);
+    const uint32_t b_bytes = (BL == BL_KN ? K : N) * g.ldb * 4;
+    const __amdgpu_buffer_rsrc_t brs[2] = {
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Bp[0]), 0, b_bytes, 0x00020000u),
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(DUAL ? Bp[1] : Bp[0]), 0, b_bytes,
+                                          0x00020000u)};
     auto load4 = [&](const float* base, uint32_t ld, uint32_t row, uint32_t rows, uint32_t col,
-                     uint32_t cols) -> float4 {
-        if (VEC)
-            return (row < rows && col < cols)
-                       ? *reinterpret_cast<const float4*>(base + (size_t)row * ld + col)
-                       : make_float4(0.f, 0.f, 0.f, 0.f);
+                     uint32_t cols, __amdgpu_buffer_rsrc_t rs) -> float4 {
+        if (VEC) {
+            const uint32_t off = (row < rows && col < cols) ? (row * ld + col) * 4 : 0x80000000u;
+            typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+            return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+        }
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
             v[e] = (row < rows && col + e < cols) ? base[(size_t)row * ld + col + e] : 0.f;
         return make_float4(v[0], v[1], v[2], v[3]);
     };
-    auto load = [&](uint32_t k0) {
+    auto load = [&](int set, uint32_t k0) {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             const uint32_t q = tid + i * NT;
             // A: 64 rows x 8 float4
-            ra[i] = load4(A, g.lda, m0 + (q >> 3), M, k0 + (q & 7) * 4, K);
-            if (RMS) ss[i] += ra[i].x * ra[i].x + ra[i].y * ra[i].y + ra[i].z * ra[i].z +
-                              ra[i].w * ra[i].w;
+            ra[set][i] = load4(A, g.lda, m0 + q / KQ, M, k0 + (q % KQ) * 4, K, ars);
 #pragma unroll
             for (int o = 0; o < NB; ++o) {
-                if (BL == BL_KN)   // B: 32 rows (k) x 16 float4 (n)
-                    rb[o][i] = load4(Bp[o], g.ldb, k0 + (q >> 4), K, n0 + (q & 15) * 4, N);
-                else               // B^T: 64 rows (n) x 8 float4 (k), like A
-                    rb[o][i] = load4(Bp[o], g.ldb, n0 + (q >> 3), N, k0 + (q & 7) * 4, K);
+                if (BL == BL_KN)   // B: BK rows (k) x 16 float4 (n)
+                    rb[set][o][i] =
+                        load4(Bp[o], g.ldb, k0 + (q >> 4), K, n0 + (q & 15) * 4, N, brs[o]);
+                else               // B^T: 64 rows (n) x KQ float4 (k), like A
+                    rb[set][o][i] =
+                        load4(Bp[o], g.ldb, n0 + q / KQ, N, k0 + (q % KQ) * 4, K, brs[o]);
             }
         }
     };
-    auto store = [&](int buf) {
+    auto store = [&](int set, int buf) {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             const uint32_t q = tid + i * NT;
-            *reinterpret_cast<float4*>(&As[buf][(q >> 3) * SA + (q & 7) * 4]) = ra[i];
+            const float4 a = ra[set][i];
+            if (RMS) ss[i] += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+            *reinterpret_cast<float4*>(&As[buf][(q / KQ) * SA + (q % KQ) * 4]) = a;
 #pragma unroll
             for (int o = 0; o < NB; ++o) {
                 if (BL == BL_KN)
-                    *reinterpret_cast<float4*>(&Bs[buf][o][(q >> 4) * SB + (q & 15) * 4]) = rb[o][i];
+                    *reinterpret_cast<float4*>(&Bs[buf][o][(q >> 4) * SB + (q & 15) * 4]) =
+                        rb[set][o][i];
                 else
-                    *reinterpret_cast<float4*>(&Bs[buf][o][(q >> 3) * SA + (q & 7) * 4]) = rb[o][i];
+                    *reinterpret_cast<float4*>(&Bs[buf][o][(q / KQ) * SA + (q % KQ) * 4]) =
+                        rb[set][o][i];
             }
         }
     };
@@ -134,47 +155,77 @@ void gemm_f32_kernel(GemmF32Args g) {
     const uint32_t li = lane & 31;     // row (A) / column (B) inside the 32x32 sub-tile
     const uint32_t lh = lane >> 5;     // which 4-wide K quarter of a group
 
+    // VEC: an even number of stages and no branch in the loop body (a stage
+    // past K multiplies the zeros its out-of-range loads stored)
+    const uint32_t nrun = VEC ? (nstages + 1) & ~1u : nstages;
     if (nstages > 0) {
-        load(0);
-        store(0);
+        load(0, 0);
+        if (VEC || nstages > 1) load(1, BK);
+        store(0, 0);
         __syncthreads();
     }
-    for (uint32_t s = 0; s < nstages; ++s) {
-        const int cur = s & 1;
-        if (s + 1 < nstages) load((s + 1) * BK);
+    // stage s: registers set s%2 were stored at the end of stage s-1, so the
+    // loads of stage s+2 reuse them; stage s+1 sits in the other set
+    auto stage = [&](uint32_t s, int cur) {
+        // past the last stage the loads are out of range (zeros, never stored)
+        if (VEC || s + 2 < nstages) load(cur, (s + 2) * BK);
+        // keep the scheduler from sinking these loads below the MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+        // Operands are double-buffered in registers: group g+1's LDS reads
+        // (and, mid-stage, the LDS stores of stage s+1) are in flight while
+        // group g's MFMAs run, so LDS traffic overlaps the MFMA pipe.
         const float* as = &As[cur][(wm * 32 + li) * SA + 4 * lh];
-#pragma unroll
-        for (int gg = 0; gg < 4 / KSPLIT; ++gg) {
-            const int gi = (int)wk * (4 / KSPLIT) + gg;
-            const float4 a4 = *reinterpret_cast<const float4*>(as + 8 * gi);
+        constexpr int NG = BK / 8 / KSPLIT;
+        float4 a4[2], b4[2][NB];
+        auto read_ops = [&](int gg, int slot) {
+            const int gi = (int)wk * NG + gg;
+            a4[slot] = *reinterpret_cast<const float4*>(as + 8 * gi);
 #pragma unroll
             for (int o = 0; o < NB; ++o) {
-                float4 b4;
                 if (BL == BL_KN) {
                     const float* bs = &Bs[cur][o][(4 * lh) * SB + wn * 32 + li];
-                    b4 = make_float4(bs[(8 * gi + 0) * SB], bs[(8 * gi + 1) * SB],
-                                     bs[(8 * gi + 2) * SB], bs[(8 * gi + 3) * SB]);
+                    b4[slot][o] = make_float4(bs[(8 * gi + 0) * SB], bs[(8 * gi + 1) * SB],
+                                              bs[(8 * gi + 2) * SB], bs[(8 * gi + 3) * SB]);
                 } else {
-                    b4 = *reinterpret_cast<const float4*>(
+                    b4[slot][o] = *reinterpret_cast<const float4*>(
                         &Bs[cur][o][(wn * 32 + li) * SA + 4 * lh + 8 * gi]);
                 }
-                acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.x, b4.x, acc[o], 0, 0, 0);
-                acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.y, b4.y, acc[o], 0, 0, 0);
-                acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.z, b4.z, acc[o], 0, 0, 0);
-                acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.w, b4.w, acc[o], 0, 0, 0);
+            }
+        };
+        read_ops(0, 0);
+#pragma unroll
+        for (int gg = 0; gg < NG; ++gg) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (gg + 1 < NG) read_ops(gg + 1, (gg + 1) & 1);
+            if (gg == NG / 2 && (VEC || s + 1 < nstages)) store(cur ^ 1, cur ^ 1);
+            __builtin_amdgcn_sched_barrier(0);
+            const int sl = gg & 1;
+#pragma unroll
+            for (int o = 0; o < NB; ++o) {
+                acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[sl].x, b4[sl][o].x, acc[o], 0, 0, 0);
+                acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[sl].y, b4[sl][o].y, acc[o], 0, 0, 0);
+                acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[sl].z, b4[sl][o].z, acc[o], 0, 0, 0);
+                acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[sl].w, b4[sl][o].w, acc[o], 0, 0, 0);
             }
         }
-        if (s + 1 < nstages) store(cur ^ 1);
+        __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
+    };
+    for (uint32_t s = 0; s < nrun; s += 2) {
+        stage(s, 0);
+        if (VEC || s + 1 < nstages) stage(s + 1, 1);
     }
 
-    if (RMS) {   // the 8 threads of an A row are 8 adjacent lanes (q & 7)
-        static_assert(LOADS == 1, "one A row per thread");
-        float t = ss[0];
-        t += __shfl_xor(t, 1);
-        t += __shfl_xor(t, 2);
-        t += __shfl_xor(t, 4);
-        if ((tid & 7) == 0 && tid < 8 * BM) rscale[tid >> 3] = rsqrtf(t / (float)K + g.eps);
+    if (RMS) {   // the KQ threads of an A row are KQ adjacent lanes (q % KQ)
+        static_assert(NT % KQ == 0 && KQ <= 64, "A rows within a wave");
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            float t = ss[i];
+#pragma unroll
+            for (int o2 = 1; o2 < KQ; o2 <<= 1) t += __shfl_xor(t, o2);
+            const uint32_t q = tid + i * NT;
+            if (q % KQ == 0) rscale[q / KQ] = rsqrtf(t / (float)K + g.eps);
+        }
     }
 
     if (KSPLIT == 2) {
@@ -223,9 +274,13 @@ int launch_variant(const GemmF32Args& g, uint32_t batch, hipStream_t s) {
         return fail(MB_E_ARG, "matmul_f32: shape too large");
     // float4 paths need 16-byte aligned rows: K % 4 for A (and B^T), N % 4 for B.
     const uintptr_t ptrs = (uintptr_t)g.a | (uintptr_t)g.b | (uintptr_t)g.b2;
+    // (and, for the buffer loads' 32-bit offsets, operands under 2 GB)
+    const uint64_t b_rows = BL == BL_KN ? g.k : g.n;
     const bool vec = (g.k % 4 == 0) && (g.lda % 4 == 0) && (g.ldb % 4 == 0) &&
                      (BL == BL_NK || g.n % 4 == 0) && (ptrs & 15) == 0 &&
-                     (g.batch_a % 4 == 0) && (g.batch_b % 4 == 0);
+                     (g.batch_a % 4 == 0) && (g.batch_b % 4 == 0) &&
+                     (uint64_t)g.m * g.lda * 4 < 0x80000000ull &&
+                     b_rows * g.ldb * 4 < 0x80000000ull;
     const dim3 grid((uint32_t)nblocks, batch), block(512);
     if (vec) hipLaunchKernelGGL((gemm_f32_kernel<2, true, BL, EPI, RMS>), grid, block, 0, s, g);
     else hipLaunchKernelGGL((gemm_f32_kernel<2, false, BL, EPI, RMS>), grid, block, 0, s, g);
