@@ -56,7 +56,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int DH = 128;        // head_dim (fixed)
 constexpr int MROWS = 16;      // MFMA rows = max batch
 constexpr int BN = 128;        // skinny GEMM column tile (W_gate | W_up: up to 4 x BN)
-constexpr int KS = 128;        // K split granularity (rows)
+constexpr int KS = 128;        // k rows of a skinny-GEMM unit with 128-column tiles
 constexpr int RING = 2;        // skinny GEMM: units in flight per workgroup
 constexpr int MAXG = 16;       // query heads per kv head (MFMA columns)
 constexpr float LOG2E = 1.4426950408889634f;
@@ -243,7 +243,7 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
     const uint32_t tile = blockIdx.x % g.tiles;
     const uint32_t split = blockIdx.x / g.tiles;
     const uint32_t k_begin = split * g.kc;
-    const uint32_t k_rows = min(g.kc, g.k - k_begin);   // a multiple of 128
+    const uint32_t k_rows = min(g.kc, g.k - k_begin);   // a multiple of 32
 
     // ---- the ring ----
     const uint32_t a_bytes = __builtin_amdgcn_readfirstlane(p.batch * g.lda * 2);
@@ -262,7 +262,9 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
     u32x4 ra[R][NTERMS];
     u32x4 rw8[R][8];
     auto issue = [&](int s, uint32_t j) {
-        const uint32_t ao = (a_row_ok && j * UR < k_rows) ? a_voff + j * UR * 2 : 0x80000000u;
+        // (a split may end inside a unit: waves past its last row read zeros)
+        const uint32_t ao =
+            (a_row_ok && j * UR + 32 * rw < k_rows) ? a_voff + j * UR * 2 : 0x80000000u;
         ra[s][0] = __builtin_amdgcn_raw_buffer_load_b128(ars0, ao, 0, 0);
         if (SPLIT_A) ra[s][NTERMS - 1] = __builtin_amdgcn_raw_buffer_load_b128(ars1, ao, 0, 0);
         const uint32_t wo = w_voff + j * UR * ldw2;
@@ -287,7 +289,7 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
 #pragma unroll
     for (int c = 0; c < 8; ++c) acc[c] = f32x4{};
     float ss = 0.f;
-    const uint32_t trips = (g.kc / UR + R - 1) / R;
+    const uint32_t trips = ((g.kc + UR - 1) / UR + R - 1) / R;
 
     for (uint32_t t = 0; t < trips; ++t) {
 #pragma unroll
@@ -852,16 +854,21 @@ struct Plan {
 
 // K split of a skinny GEMM: enough splits that tiles x splits gives about one
 // workgroup per CU (fewer, longer streams read HBM faster than two per CU),
-// each split a whole number of 128-row steps; the ring holds RING units of
-// 128 / ww rows, or the split's unit count below that.
-static void choose_split(uint32_t tiles, uint32_t ksteps, uint32_t ww, uint32_t* splits,
-                         uint32_t* kc, uint32_t* ring) {
+// each split a whole number of 32-row groups (so 5 splits of K = 4096 are
+// 832, 832, 832, 832 and 768 rows rather than 7, 7, 7, 7 and 4 steps of 128);
+// the ring holds RING units of 128 / ww rows, or the split's unit count below
+// that.
+constexpr uint32_t KG = 32;   // K split granularity (rows)
+
+static void choose_split(uint32_t tiles, uint32_t k, uint32_t ww, uint32_t* splits, uint32_t* kc,
+                         uint32_t* ring) {
+    const uint32_t groups = k / KG;
     const uint32_t slots = std::max(device_cu_count(), 1u);
-    const uint32_t want = std::min(std::max(1u, slots / tiles), ksteps);
-    const uint32_t per = cdiv(ksteps, want);
-    *splits = cdiv(ksteps, per);
-    *kc = per * KS;
-    const uint32_t units = per * ww;
+    const uint32_t want = std::min(std::max(1u, slots / tiles), groups);
+    const uint32_t per = cdiv(groups, want);
+    *splits = cdiv(groups, per);
+    *kc = per * KG;
+    const uint32_t units = cdiv(*kc, KS / ww);
     *ring = units >= RING ? RING : (units >= 2 ? 2 : 1);
 }
 
@@ -914,10 +921,10 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
     const uint32_t ldw[4] = {pl->nqkv, D, 2 * FF, D};
     for (int i = 0; i < 4; ++i) {
         const uint32_t k = i == EPI_DOWN ? FF : D;
-        choose_split(pl->tiles[i], k / KS, pl->ww[i], &pl->splits[i], &pl->kc[i], &pl->ring[i]);
+        choose_split(pl->tiles[i], k, pl->ww[i], &pl->splits[i], &pl->kc[i], &pl->ring[i]);
         // the ring's clipped loads run up to RING units past the split
         const uint64_t unit = KS / pl->ww[i];
-        const uint64_t trips = cdiv(pl->kc[i] / (uint32_t)unit, pl->ring[i]);
+        const uint64_t trips = cdiv(cdiv(pl->kc[i], (uint32_t)unit), pl->ring[i]);
         if ((trips + 1) * pl->ring[i] * unit * ldw[i] * 2 > 0xffffffffull ||
             (uint64_t)B * k * 2 >= 0x80000000ull)
             return fail(MB_E_ARG, "decoder step: shapes too large for 32-bit weight offsets");
