@@ -35,6 +35,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 64, BN = 64, BK = 32;
 constexpr int SK = BK + 4;   // LDS row stride (floats), both operands
+constexpr int KQ = BK / 4;   // float4s per K-contiguous row of a stage
 
 struct ConvShape {
     uint32_t n, h, w, c, o, r, s, stride, pad, p, q;
@@ -62,14 +63,14 @@ void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt
     const uint32_t m0 = tm * BM, n0 = tn * BN;
     const uint32_t nstages = (sh.k + BK - 1) / BK;
 
-    // Per-thread rows of the A tile: row = q >> 3 (q = tid + i*NT), float4 column q & 7.
+    // Per-thread rows of the A tile: row = q / KQ (q = tid + i*NT), float4 column q % KQ.
     // Hoisted im2col decomposition: pixel (n, p, q) -> image base and top-left tap.
     int32_t row_h0[LOADS], row_w0[LOADS];
     uint64_t row_base[LOADS];
     bool row_ok[LOADS];
 #pragma unroll
     for (int i = 0; i < LOADS; ++i) {
-        const uint32_t m = m0 + ((tid + i * NT) >> 3);
+        const uint32_t m = m0 + (tid + i * NT) / KQ;
         row_ok[i] = m < sh.m;
         const uint32_t mm = row_ok[i] ? m : 0;
         const uint32_t qq = mm % sh.q;
@@ -100,7 +101,7 @@ void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt
             const uint32_t r = rs / sh.s, s = rs - r * sh.s;
 #pragma unroll
             for (int i = 0; i < LOADS; ++i) {
-                const uint32_t q4 = ((tid + i * NT) & 7) * 4;
+                const uint32_t q4 = ((tid + i * NT) % KQ) * 4;
                 const int32_t hi = row_h0[i] + (int32_t)r, wi = row_w0[i] + (int32_t)s;
                 const bool in = row_ok[i] && k0 < sh.k && hi >= 0 && hi < (int32_t)sh.h &&
                                 wi >= 0 && wi < (int32_t)sh.w;
@@ -112,7 +113,7 @@ void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt
         } else {
 #pragma unroll
             for (int i = 0; i < LOADS; ++i) {
-                const uint32_t q4 = ((tid + i * NT) & 7) * 4;
+                const uint32_t q4 = ((tid + i * NT) % KQ) * 4;
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -133,7 +134,7 @@ void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             const uint32_t q = tid + i * NT;
-            const uint32_t oc = n0 + (q >> 3), kq = k0 + (q & 7) * 4;
+            const uint32_t oc = n0 + q / KQ, kq = k0 + (q % KQ) * 4;
             if (FAST) {
                 rb[set][i] = ld4(wrs, (oc < sh.o && kq < sh.k) ? (oc * sh.k + kq) * 4 : 0x80000000u);
             } else {
@@ -149,8 +150,8 @@ void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             const uint32_t q = tid + i * NT;
-            *reinterpret_cast<float4*>(&As[buf][(q >> 3) * SK + (q & 7) * 4]) = ra[set][i];
-            *reinterpret_cast<float4*>(&Bs[buf][(q >> 3) * SK + (q & 7) * 4]) = rb[set][i];
+            *reinterpret_cast<float4*>(&As[buf][(q / KQ) * SK + (q % KQ) * 4]) = ra[set][i];
+            *reinterpret_cast<float4*>(&Bs[buf][(q / KQ) * SK + (q % KQ) * 4]) = rb[set][i];
         }
     };
 
