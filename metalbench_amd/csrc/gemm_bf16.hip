@@ -7,23 +7,25 @@
 // at bf16, rounded to bf16 (round to nearest even) once, from fp32.
 //
 // gfx950 design (MFMA bound: 2*M*N*K flops vs 2*(MK+KN+MN) bytes):
-//  * workgroup tile 256x256, BK = 64, 4 waves in a 2x2 grid, each wave a
-//    128x128 sub-tile = 4x4 v_mfma_f32_32x32x16_bf16 accumulators (256 fp32
-//    per lane, held in AccVGPRs); one workgroup per CU, 1024 tiles at 8192^3 =
+//  * workgroup tile 256x256, 4 waves in a 2x2 grid, each wave a 128x128
+//    sub-tile = 4x4 v_mfma_f32_32x32x16_bf16 accumulators (256 fp32 per
+//    lane, held in AccVGPRs); one workgroup per CU, 1024 tiles at 8192^3 =
 //    exactly four rounds of 256 CUs;
-//  * (the guarded / element-wise kernel; the full-tile kernel further down
-//    keeps the tile shape but swizzles A and stages loads two ahead)
-//    LDS double buffer: both operands stored K-contiguous, row pitch 72 bf16
-//    (144 B), 2 x 2 x 36 KB = 144 KB of the 160 KB.  With that pitch the MFMA
-//    operand reads (ds_read_b128 of 16 consecutive rows) and both store
-//    patterns below touch distinct bank groups;
-//  * A is row-major [M][K], already K-contiguous: 16-byte global loads go
-//    straight to LDS rows;
-//  * B is row-major [K][N] (N-contiguous), but the MFMA B operand wants 8
+//  * full tiles (the large_mm shape) take gemm_bf16_full_kernel further down:
+//    both operands go global -> LDS by DMA into a four-stage ring (no staging
+//    registers, no LDS store instructions) and B is transposed by the LDS
+//    reads (ds_read_b64_tr_b16);
+//  * other shapes take gemm_bf16_kernel, BK = 64 with an LDS double buffer:
+//    both operands stored K-contiguous, row pitch 72 bf16 (144 B), 2 x 2 x
+//    36 KB = 144 KB of the 160 KB.  With that pitch the MFMA operand reads
+//    (ds_read_b128 of 16 consecutive rows) and both store patterns below
+//    touch distinct bank groups.  A is row-major [M][K], already
+//    K-contiguous: 16-byte global loads go straight to LDS rows.  B is
+//    row-major [K][N] (N-contiguous), but the MFMA B operand wants 8
 //    consecutive k per lane: each lane loads an 8(k) x 8(n) block as eight
-//    16-byte rows, transposes it in registers with 32 v_perm_b32 (pairing
-//    k and k+1 halves into dwords) and stores eight K-contiguous 16-byte rows;
-//  * global loads of stage s+1 are issued before the MFMAs of stage s, and
+//    16-byte rows, transposes it in registers with 32 v_perm_b32 (pairing k
+//    and k+1 halves into dwords) and stores eight K-contiguous 16-byte rows.
+//    Global loads of stage s+1 are issued before the MFMAs of stage s, and
 //    the LDS operand reads of k-step kk+1 are in flight during the MFMAs of kk;
 //  * XCD-aware tile order: hardware dispatches block b to XCD b % 8, so the
 //    block id is remapped so that each XCD walks one band of GM = 4 tile-rows
@@ -216,26 +218,62 @@ void gemm_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
 }
 
 // ---- full-tile kernel (M, N multiples of 256, K of 128, operands < 2 GiB) ----
-// Both operands are register-staged TWO LDS stages ahead: the global loads
-// for stage s+2 are issued during the MFMAs of stage s, so a load has about
-// 2 x 64 MFMAs per wave (~4 us at the power-limited clock) to arrive.
-//  * A rows are stored unpadded (128 B = 8 chunks of 8 k) with chunk c of row
-//    r in slot c ^ ((r / 2) % 8): a ds_read_b128 serves 16 lanes = 16
-//    consecutive rows per LDS cycle, and their 16-byte bank groups
-//    8 (r % 2) + slot are then all distinct (conflict free);
-//  * B (N-contiguous in HBM) is loaded as 8 x 16-byte rows per lane,
-//    transposed in registers with v_perm_b32 and stored K-contiguous into
-//    the pitch-72 layout;
-//  * stage s: loads of stage s+2 -> register set s % 2 (A in k steps 0-1, B
-//    in k steps 2-3, 4 loads per 16 MFMAs), MFMAs on LDS buffers s % 2, and
-//    in k step 3 the stores of register set (s+1) % 2 into buffers
-//    (s+1) % 2; then an LDS-only barrier (lgkmcnt + s_barrier, the global
-//    loads stay in flight).  sched_group_barrier interleaves one MFMA with
-//    each group of loads / operand reads / transposes / stores, so the MFMA
-//    pipe never waits on issue.
-// Buffer-to-LDS DMA for A (no registers, no LDS store instructions) was
-// measured slower than this on MI355X (49% vs 50.6% of peak at 8192^3).
-constexpr int ROWB = BK * 2;              // bytes per unpadded A row in LDS
+// Both operands go global -> LDS by DMA (buffer_load ... lds): no staging
+// registers and no LDS store instructions, whose VGPR reads stall the MFMA
+// issue.  The LDS holds a ring of four 32-deep k stages (A 16 KB + B 16 KB
+// each), so a stage's DMAs are issued three stages before its MFMAs:
+//  * A [256 rows][32 k], 64-byte rows; chunk c (8 k) of row r sits in slot
+//    c ^ ((r / 4) % 4).  A ds_read_b128 serves 16 lanes = 16 consecutive
+//    rows per LDS cycle, whose 16-byte bank groups 4 (r % 4) + slot are then
+//    all distinct;
+//  * B [32 k][256 n] row-major as in HBM, 512-byte rows; chunk c (8 n) of
+//    k-row r sits in slot c ^ (4 (r % 4)).  The MFMA B operand (8
+//    consecutive k of one column) is two ds_read_b64_tr_b16: in each 16-lane
+//    group lane s points at k-row k0 + s/4, columns n0 + 4 (s % 4) .. +3,
+//    and lane s receives column n0 + s, k-rows k0 .. k0+3;
+//  * each DMA instruction writes a wave's 64 x 16 B contiguously, so lane l
+//    fetches the global chunk that its slot holds.
+// Stage s (buffer s % 4): k step 0 reads the operands of k step 1 under its
+// 16 MFMAs; k step 1 waits for this wave's DMAs of stage s+1, passes an
+// LDS barrier (every wave has then read all of stage s, and every wave's
+// stage s+1 DMAs have landed), refills buffer s % 4 with stage s+4 and reads
+// stage s+1's first operands under its 16 MFMAs.  The operands of k step 1
+// are already in registers when its barrier passes, and the DMAs have three
+// stages (~1.5 us) to land.
+// Measured on MI355X against the previous design (both operands staged in
+// registers two stages ahead, B transposed with v_perm_b32, ds_write_b128
+// into a padded double buffer): MFMA busy 73 % -> 85 % of the kernel's
+// cycles and 6-10 % less time per 8192^3 launch.  The LDS store instructions
+// were what stalled the MFMA issue (removing only them gave 91 %).
+constexpr int KS = 32;                    // k per LDS stage
+constexpr int AROWB = KS * 2;             // bytes per A row in LDS
+constexpr int BROWB = BN * 2;             // bytes per B k-row in LDS
+constexpr int STAGE_A = BM * KS;          // bf16 per A stage
+constexpr int STAGE_ELEMS = STAGE_A + KS * BN;
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer descriptor in SGPRs (raw, stride 0) for the DMA below.
+__device__ __forceinline__ i32x4 dma_rsrc(const void* p, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    return i32x4{(int32_t)__builtin_amdgcn_readfirstlane((uint32_t)a),
+                 (int32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu),
+                 (int32_t)__builtin_amdgcn_readfirstlane(bytes), 0x00020000};
+}
+
+// 16 bytes per lane global -> LDS (lane l lands at lds_addr + 16 l).  Written
+// as asm so that the compiler's wait-count pass, which cannot tell which ring
+// buffer a DMA targets, does not add vmcnt(0) waits before every LDS read; the
+// kernel waits for its DMAs itself.
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :: "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff) : "m0");
+}
 
 __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -247,10 +285,10 @@ __global__ __launch_bounds__(256, 1)
 void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                            uint16_t* __restrict__ C, uint32_t M, uint32_t N, uint32_t K,
                            uint32_t tiles_m, uint32_t tiles_n) {
-    __shared__ __attribute__((aligned(1024))) uint16_t As0[BM * BK];
-    __shared__ __attribute__((aligned(1024))) uint16_t As1[BM * BK];
-    __shared__ __attribute__((aligned(16))) uint16_t Bs0[TILE_ELEMS];
-    __shared__ __attribute__((aligned(16))) uint16_t Bs1[TILE_ELEMS];
+    __shared__ __attribute__((aligned(1024))) uint16_t L0[STAGE_ELEMS];
+    __shared__ __attribute__((aligned(1024))) uint16_t L1[STAGE_ELEMS];
+    __shared__ __attribute__((aligned(1024))) uint16_t L2[STAGE_ELEMS];
+    __shared__ __attribute__((aligned(1024))) uint16_t L3[STAGE_ELEMS];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63;
@@ -260,55 +298,33 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
     tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, &tm, &tn);
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(tm * BM);
     const uint32_t n0 = __builtin_amdgcn_readfirstlane(tn * BN);
-    const uint32_t nstages = K / BK;
-    const uint32_t last_k0 = (nstages - 1) * BK;
+    const uint32_t nstages = K / KS;   // a multiple of 4
+    const uint32_t last_k0 = (nstages - 1) * KS;
 
-    const __amdgpu_buffer_rsrc_t ars =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A), 0, M * K * 2, 0x00020000u);
-    const __amdgpu_buffer_rsrc_t brs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(B), 0, K * N * 2, 0x00020000u);
+    const i32x4 ars = dma_rsrc(A, M * K * 2), brs = dma_rsrc(B, K * N * 2);
 
-    // A: lane loads rows a_row + 32 i (i < 8), 16-byte chunk a_chunk, and
-    // stores them into the swizzled layout (slot = chunk ^ ((row / 2) % 8)).
-    const uint32_t a_row = tid >> 3, a_chunk = tid & 7;
-    const uint32_t a_voff = (a_row * K + 8 * a_chunk) * 2;
-    u32x4 ra[2][8];
-    auto load_a = [&](int st, uint32_t k0, int i0, int i1) {
-#pragma unroll
-        for (int i = i0; i < i1; ++i)
-            ra[st][i] = __builtin_amdgcn_raw_buffer_load_b128(ars, a_voff, ((m0 + 32 * i) * K + k0) * 2, 0);
+    // A DMA: instruction i of wave w fills rows 64 w + 16 i + l/4, slot l%4,
+    // which holds chunk (l%4) ^ ((l/16) % 4).
+    const uint32_t a_voff = ((lane >> 2) * K + 8 * ((lane & 3) ^ ((lane >> 4) & 3))) * 2;
+    // B DMA: instruction i of wave w fills k-rows 8 w + 2 i + l/32, slot l%32,
+    // which holds chunk (l%32) ^ (4 ((2 i + l/32) % 4)).
+    const uint32_t b_r = lane >> 5;
+    const uint32_t b_voff0 = (b_r * N + 8 * ((lane & 31) ^ (4 * b_r))) * 2;
+    const uint32_t b_voff1 = (b_r * N + 8 * ((lane & 31) ^ (4 * (2 + b_r)))) * 2;
+    // LDS byte addresses of the ring buffers and of this wave's DMA targets.
+    const uint32_t ring[4] = {(uint32_t)(uintptr_t)(lds_void_t*)L0, (uint32_t)(uintptr_t)(lds_void_t*)L1,
+                              (uint32_t)(uintptr_t)(lds_void_t*)L2, (uint32_t)(uintptr_t)(lds_void_t*)L3};
+    const uint32_t a_dst = 64 * wave * AROWB, b_dst = STAGE_A * 2 + 8 * wave * BROWB;
+    const uint32_t a_src = (m0 + 64 * wave) * K * 2, b_src = (8 * wave * N + n0) * 2;
+    // DMA instructions i (A) and i (B) of stage k0 into ring buffer rb.
+    auto dma_part = [&](int rb, uint32_t k0, int i) {
+        dma16(ars, ring[rb] + a_dst + 16 * i * AROWB, a_voff, a_src + (16 * i * K + k0) * 2);
+        dma16(brs, ring[rb] + b_dst + 2 * i * BROWB, (i & 1) ? b_voff1 : b_voff0,
+              b_src + (k0 + 2 * i) * N * 2);
     };
-    auto store_a = [&](int st, uint16_t* as_dst) {
-        uint8_t* as = reinterpret_cast<uint8_t*>(as_dst);
+    auto dma = [&](int rb, uint32_t k0) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t row = a_row + 32 * i;
-            *reinterpret_cast<u32x4*>(as + row * ROWB + 16 * (a_chunk ^ ((row >> 1) & 7))) = ra[st][i];
-        }
-    };
-    // B: k-octet ko = tid%8, n-octet no = tid/8 (8 rows of 16 B each).
-    const uint32_t b_ko = tid & 7, b_no = tid >> 3;
-    const uint32_t b_voff = (8 * b_ko * N + 8 * b_no) * 2;
-    u32x4 rb[2][8];
-    auto load_b = [&](int st, uint32_t k0, int r0, int r1) {   // rows [r0, r1)
-#pragma unroll
-        for (int r = r0; r < r1; ++r)
-            rb[st][r] = __builtin_amdgcn_raw_buffer_load_b128(brs, b_voff, ((k0 + r) * N + n0) * 2, 0);
-    };
-    auto store_b = [&](int st, uint16_t* bs) {
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            uint32_t lo[4], hi[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                lo[j] = __builtin_amdgcn_perm(rb[st][2 * j + 1][m], rb[st][2 * j][m], 0x05040100u);
-                hi[j] = __builtin_amdgcn_perm(rb[st][2 * j + 1][m], rb[st][2 * j][m], 0x07060302u);
-            }
-            *reinterpret_cast<u32x4*>(bs + (8 * b_no + 2 * m) * PITCH + 8 * b_ko) =
-                u32x4{lo[0], lo[1], lo[2], lo[3]};
-            *reinterpret_cast<u32x4*>(bs + (8 * b_no + 2 * m + 1) * PITCH + 8 * b_ko) =
-                u32x4{hi[0], hi[1], hi[2], hi[3]};
-        }
+        for (int i = 0; i < 4; ++i) dma_part(rb, k0, i);
     };
 
     f32x16 acc[4][4];
@@ -318,113 +334,111 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
     const uint32_t li = lane & 31, lh = lane >> 5;
-    // One LDS stage of MFMAs.  The next stages' global loads are spread over
-    // the four k steps (`pre(kk)` issues a quarter: 4 loads per 16 MFMAs, so
-    // the texture unit never backs up into the wave's in-order issue), and
-    // `post` (the B transpose + LDS stores of the next stage) runs inside k
-    // step 3; one instruction group per MFMA, so nothing but the initial
-    // operand reads sits outside the MFMA shadow.
-    auto mfma_stage = [&](const uint16_t* as_base, const uint16_t* bs_base, auto&& pre,
-                          auto&& post) {
-        const uint8_t* as = reinterpret_cast<const uint8_t*>(as_base) + (wm * 128 + li) * ROWB;
-        const uint16_t* bs = bs_base + (wn * 128 + li) * PITCH + 8 * lh;
-        auto a_at = [&](int i, int kk) {   // rows wm*128 + 32 i + li, k chunk 2 kk + lh, swizzled
-            return *reinterpret_cast<const bf16x8*>(as + 32 * i * ROWB +
-                                                    16 * ((2 * kk + lh) ^ ((li >> 1) & 7)));
+    // A operand (i, kk): row wm*128 + 32 i + li, chunk 2 kk + lh, in slot
+    // chunk ^ ((li/4) % 4).
+    const uint32_t a_row = (wm * 128 + li) * AROWB, a_sw = (li >> 2) & 3;
+    // B operand (j, kk), half q: k-row 16 kk + 4 q + tr_row, column
+    // tr_col + 32 j (tr_row % 4 = (l/4) % 4 for every kk, q).
+    const uint32_t tr_row = 8 * lh + ((lane & 15) >> 2);
+    const uint32_t tr_col = wn * 128 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    uint32_t b_off[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t c = tr_col + 32 * j;
+        b_off[j] = tr_row * BROWB + 16 * ((c >> 3) ^ (4 * (tr_row & 3))) + 2 * (c & 7);
+    }
+    auto b_at = [&](const uint8_t* bs, int j, int kk) {
+        u32x2 h[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+            h[q] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4_t*)(bs + b_off[j] + (16 * kk + 4 * q) * BROWB)));
+        return __builtin_bit_cast(bf16x8, u32x4{h[0][0], h[0][1], h[1][0], h[1][1]});
+    };
+    bf16x8 a[2][4], b[2][4];
+    auto read_ops = [&](const uint16_t* buf, int kk, int c) {   // order a0, b0..b3, a1..a3
+        const uint8_t* as = reinterpret_cast<const uint8_t*>(buf) + a_row;
+        const uint8_t* bs = reinterpret_cast<const uint8_t*>(buf + STAGE_A);
+        auto a_at = [&](int i) {
+            return *reinterpret_cast<const bf16x8*>(as + 32 * i * AROWB + 16 * ((2 * kk + lh) ^ a_sw));
         };
-        bf16x8 a[2][4], b[2][4];
+        a[c][0] = a_at(0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) a[0][i] = a_at(i, 0);
+        for (int j = 0; j < 4; ++j) b[c][j] = b_at(bs, j, kk);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) b[0][j] = *reinterpret_cast<const bf16x8*>(bs + 32 * j * PITCH);
+        for (int i = 1; i < 4; ++i) a[c][i] = a_at(i);
+    };
+    auto mfmas = [&](int c) {
 #pragma unroll
-        for (int kk = 0; kk < BK / 16; ++kk) {
-            const int c = kk & 1;
-            __builtin_amdgcn_sched_barrier(0);
-            pre(kk);
-            if (kk + 1 < BK / 16) {
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) a[c ^ 1][i] = a_at(i, kk + 1);
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[c][i], b[c][j], acc[i][j], 0, 0, 0);
+    };
+    // One stage on ring buffer rc (pointer cur); `kdma` is the k of the stage
+    // that refills it.  k step 1 is four chunks, each: two DMAs, three
+    // operand reads of the next stage (a_q, b_q), four MFMAs (row block q).
+    auto stage = [&](int rc, const uint16_t* cur, const uint16_t* nxt, uint32_t kdma) {
+        __builtin_amdgcn_sched_barrier(0);
+        read_ops(cur, 1, 1);
+        mfmas(0);
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    b[c ^ 1][j] = *reinterpret_cast<const bf16x8*>(bs + 32 * j * PITCH + 16 * (kk + 1));
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[c][i], b[c][j], acc[i][j],
-                                                                         0, 0, 0);
-            if (kk == BK / 16 - 1) post();
-            if (kk + 1 < BK / 16) {   // 16 MFMA, 8 operand reads, 4 global loads
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
-                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
-                    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
-                }
-            } else {                  // 16 MFMA, 4 global loads, 32 v_perm + 16 LDS stores
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read
-                    __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);   // DS write
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
-                    __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // DS write
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
-                    __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // DS write
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                }
-            }
+        for (int q = 0; q < 4; ++q) {   // 16 MFMA, 12 operand reads
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
         }
         __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0x4F70);   // vmcnt(16): stages s+2, s+3 may be in flight
+        lds_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t* nas = reinterpret_cast<const uint8_t*>(nxt) + a_row;
+        const uint8_t* nbs = reinterpret_cast<const uint8_t*>(nxt + STAGE_A);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            dma_part(rc, kdma, q);
+            __builtin_amdgcn_sched_barrier(0);
+            a[0][q] = *reinterpret_cast<const bf16x8*>(nas + 32 * q * AROWB + 16 * (lh ^ a_sw));
+            b[0][q] = b_at(nbs, q, 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[q][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][q], b[1][j], acc[q][j], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
 
-    load_a(0, 0, 0, 8);
-    load_b(0, 0, 0, 8);
-    __builtin_amdgcn_s_waitcnt(0);
-    store_a(0, As0);
-    store_b(0, Bs0);
-    __syncthreads();
-    load_a(1, min((uint32_t)BK, last_k0), 0, 8);
-    load_b(1, min((uint32_t)BK, last_k0), 0, 8);
-    // Stage s: MFMAs on buffers s % 2; register set s % 2 receives stage s+2
-    // (A in k steps 0-1, B in 2-3); set (s+1) % 2, loaded one stage earlier,
-    // is stored to the other buffers inside k step 3.  nstages is even
-    // (K % 128 == 0), so the body is straight-line: past the last stage the
-    // clamped loads re-read it and land in buffers never read again.
-    for (uint32_t s = 0; s < nstages; s += 2) {
-        const uint32_t k2 = min((s + 2) * BK, last_k0), k3 = min((s + 3) * BK, last_k0);
-        mfma_stage(As0, Bs0,
-                   [&](int kk) {
-                       if (kk < 2) load_a(0, k2, 4 * kk, 4 * kk + 4);
-                       else load_b(0, k2, 4 * (kk - 2), 4 * (kk - 2) + 4);
-                   },
-                   [&] { store_a(1, As1); store_b(1, Bs1); });
-        lds_barrier();
-        mfma_stage(As1, Bs1,
-                   [&](int kk) {
-                       if (kk < 2) load_a(1, k3, 4 * kk, 4 * kk + 4);
-                       else load_b(1, k3, 4 * (kk - 2), 4 * (kk - 2) + 4);
-                   },
-                   [&] { store_a(0, As0); store_b(0, Bs0); });
-        lds_barrier();
+    dma(0, 0);
+    dma(1, KS);
+    dma(2, 2 * KS);
+    dma(3, 3 * KS);
+    __builtin_amdgcn_s_waitcnt(0x4F78);   // vmcnt(24): stage 0 has landed
+    lds_barrier();
+    read_ops(L0, 0, 0);
+    // nstages % 4 == 0, so the body is straight-line; past the last stage the
+    // clamped DMAs re-read it into buffers that are never read again.
+    for (uint32_t s = 0; s < nstages; s += 4) {
+        stage(0, L0, L1, min((s + 4) * KS, last_k0));
+        stage(1, L1, L2, min((s + 5) * KS, last_k0));
+        stage(2, L2, L3, min((s + 6) * KS, last_k0));
+        stage(3, L3, L0, min((s + 7) * KS, last_k0));
     }
-
+    __builtin_amdgcn_s_waitcnt(0);   // no DMA may still target LDS
 
     // Epilogue through LDS: each wave converts its 128 x 128 tile to bf16
     // (hardware round-to-nearest-even convert), writes it row-major into its
-    // own 32 KB of the now idle operand buffers, and streams it out as 16-byte
-    // row chunks (a wave store instruction covers four 256-byte row segments).
+    // own 32 KB buffer of the ring, and streams it out as 16-byte row chunks
+    // (a wave store instruction covers four 256-byte row segments).
     // Lane l, reg r of 32x32 block (i, j): row 32 i + 8 (r/4) + 4 (l/32) + r%4,
     // column 32 j + l%32.
     lds_barrier();   // every wave is done reading the operand buffers
-    uint16_t* ct = wave == 0 ? As0 : wave == 1 ? As1 : wave == 2 ? Bs0 : Bs1;
+    uint16_t* ct = wave == 0 ? L0 : wave == 1 ? L1 : wave == 2 ? L2 : L3;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
