@@ -113,6 +113,41 @@ enum GemmF32Kind {
     GEMM_F32_PLAIN, GEMM_F32_RMS, GEMM_F32_RMS_BT, GEMM_F32_RESID, GEMM_F32_SWIGLU,
     GEMM_F32_RMS_SWIGLU
 };
+// ---- global -> LDS DMA ------------------------------------------------------
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Buffer descriptor in SGPRs (raw, stride 0) for dma16.
+__device__ __forceinline__ i32x4 dma_rsrc(const void* p, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(p);
+    return i32x4{(int32_t)__builtin_amdgcn_readfirstlane((uint32_t)a),
+                 (int32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu),
+                 (int32_t)__builtin_amdgcn_readfirstlane(bytes), 0x00020000};
+}
+
+// 16 bytes per lane global -> LDS (lane l lands at lds_addr + 16 l).  Written
+// as asm so that the compiler's wait-count pass, which cannot tell which LDS
+// buffer a DMA targets, does not add vmcnt(0) before every LDS read; callers
+// wait for their DMAs themselves (s_waitcnt vmcnt) and publish them with a
+// barrier.
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :: "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff) : "m0");
+}
+
+// Workgroup barrier that orders LDS only (lgkmcnt + s_barrier): global loads
+// and DMAs in flight stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// LDS address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const lds_void_t*)p;
+}
+
 // Dense row-major defaults: lda = k, ldb = ldc = ldr = n, no batch stride.
 GemmF32Args gemm_f32_args(const float* a, const float* b, float* c, uint32_t m, uint32_t n,
                           uint32_t k);

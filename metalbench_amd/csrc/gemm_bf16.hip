@@ -253,33 +253,8 @@ constexpr int STAGE_ELEMS = STAGE_A + KS * BN;
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
 
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-
-// Buffer descriptor in SGPRs (raw, stride 0) for the DMA below.
-__device__ __forceinline__ i32x4 dma_rsrc(const void* p, uint32_t bytes) {
-    const uint64_t a = reinterpret_cast<uint64_t>(p);
-    return i32x4{(int32_t)__builtin_amdgcn_readfirstlane((uint32_t)a),
-                 (int32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu),
-                 (int32_t)__builtin_amdgcn_readfirstlane(bytes), 0x00020000};
-}
-
-// 16 bytes per lane global -> LDS (lane l lands at lds_addr + 16 l).  Written
-// as asm so that the compiler's wait-count pass, which cannot tell which ring
-// buffer a DMA targets, does not add vmcnt(0) waits before every LDS read; the
-// kernel waits for its DMAs itself.
-__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                 :: "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff) : "m0");
-}
-
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 __global__ __launch_bounds__(256, 1)
 void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,

@@ -41,6 +41,8 @@
 //    multiplies), so the normalised rows are never materialised.
 #include "common.h"
 
+#include <type_traits>
+
 namespace mb {
 namespace {
 
@@ -267,6 +269,145 @@ void gemm_f32_kernel(GemmF32Args g) {
     }
 }
 
+// Full-tile kernel for C = A B: M, N multiples of 64, K of 256, B [K][N],
+// 16-byte aligned rows, operands under 2 GB.  Same tile, waves and MFMA as
+// gemm_f32_kernel<2, true, BL_KN, EPI_STORE, false>, but the operands go
+// global -> LDS by DMA (buffer_load ... lds) into a ring of four 64-deep k
+// stages (A 16 KB + B 16 KB each): no staging registers and no LDS store
+// instructions, whose VGPR reads held the MFMA pipe to ~72 % busy (~91 %
+// with them removed).
+//  * A slot: [64 rows][64 k], 256-byte rows; 16-byte chunk c of row r sits in
+//    slot c ^ (r % 16), so a ds_read_b128 of 16 consecutive rows touches 16
+//    distinct bank groups;
+//  * B slot: [64 k][64 n], 256-byte k-rows; chunk c of k-row r sits in slot
+//    c ^ (8 ((r / 4) % 2)), so the two half-waves' ds_read_b32 (k-rows r and
+//    r + 4, the same 32 columns) fall in opposite halves of the bank window;
+//  * a DMA instruction writes a wave's 64 x 16 B = four rows contiguously, so
+//    lane l fetches the global chunk that its slot holds; each of the 8 waves
+//    issues 2 A and 2 B instructions per stage;
+//  * stage s (slot s % 4): groups 0-2 read the next group's operands under
+//    the current group's 4 MFMAs; before group 3 the wave waits for its DMAs
+//    of stage s+1 (vmcnt(8): stages s+2 and s+3 stay in flight), passes a
+//    barrier (every wave has read all of stage s; every wave's stage s+1 DMAs
+//    have landed), refills slot s % 4 with stage s+4 and reads stage s+1's
+//    first operands under group 3's MFMAs.
+constexpr int F_SLOT = BM * BK;              // floats per operand per stage slot (16 KB)
+
+__global__ __launch_bounds__(512)
+void gemm_f32_dma_kernel(GemmF32Args g) {
+    __shared__ __attribute__((aligned(1024))) float L[4][2 * F_SLOT];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wk = wave >> 2, wm = (wave >> 1) & 1, wn = wave & 1;
+    const uint32_t tm = blockIdx.x / g.tiles_n;
+    const uint32_t tn = blockIdx.x - tm * g.tiles_n;
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(tm * BM);
+    const uint32_t n0 = __builtin_amdgcn_readfirstlane(tn * BN);
+    const uint32_t N = g.n, K = g.k, lda = g.lda, ldb = g.ldb;
+    const uint32_t nstages = K / BK;   // a multiple of 4
+    const uint32_t last_k0 = K - BK;
+    const float* A = g.a + (size_t)blockIdx.y * g.batch_a;
+    const float* B = g.b + (size_t)blockIdx.y * g.batch_b;
+    float* C = g.c + (size_t)blockIdx.y * g.batch_c;
+
+    const i32x4 ars = dma_rsrc(A, g.m * lda * 4), brs = dma_rsrc(B, K * ldb * 4);
+    // DMA instruction i (0, 1) of wave w: rows (A) / k-rows (B) 8 w + 4 i + l/16, slot l%16.
+    const uint32_t r4 = lane >> 4, sl = lane & 15;
+    uint32_t a_voff[2], b_voff[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        a_voff[i] = (r4 * lda + 4 * (sl ^ ((8 * (wave & 1) + 4 * i + r4) & 15))) * 4;
+        b_voff[i] = (r4 * ldb + 4 * (sl ^ (8 * i))) * 4;
+    }
+    const uint32_t l0 = lds_addr(&L[0][0]);
+    auto dma = [&](int slot, uint32_t k0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t r = 8 * wave + 4 * i;
+            dma16(ars, l0 + slot * (8 * F_SLOT) + r * 256, a_voff[i], ((m0 + r) * lda + k0) * 4);
+            dma16(brs, l0 + slot * (8 * F_SLOT) + 4 * F_SLOT + r * 256, b_voff[i],
+                  ((k0 + r) * ldb + n0) * 4);
+        }
+    };
+
+    const uint32_t li = lane & 31, lh = lane >> 5;
+    // A operand of group gi (8 k): row wm*32 + li, chunk 2 gi + lh, swizzled.
+    const uint32_t a_row = (wm * 32 + li) * 256, a_sw = li & 15;
+    // B operand of group gi, t = 0..3: k-row 8 gi + 4 lh + t, column wn*32 + li
+    // (chunk wn*8 + li/4 ^ 8 lh, float li % 4).
+    const uint32_t b_col = 16 * ((wn * 8 + (li >> 2)) ^ (8 * lh)) + 4 * (li & 3) + 4 * lh * 256;
+    const uint8_t* l8 = reinterpret_cast<const uint8_t*>(&L[0][0]);
+    float4 a4[2], b4[2];
+    auto read_ops = [&](int slot, int gg, int c) {
+        const int gi = (int)wk * 4 + gg;
+        const uint8_t* base = l8 + slot * (8 * F_SLOT);
+        a4[c] = *reinterpret_cast<const float4*>(base + a_row + 16 * ((2 * gi + lh) ^ a_sw));
+        const float* bp = reinterpret_cast<const float*>(base + 4 * F_SLOT + 8 * gi * 256 + b_col);
+        b4[c] = make_float4(bp[0], bp[64], bp[128], bp[192]);
+    };
+    f32x16 acc = f32x16{};
+    auto mfma4 = [&](int c) {
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[c].x, b4[c].x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[c].y, b4[c].y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[c].z, b4[c].z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[c].w, b4[c].w, acc, 0, 0, 0);
+    };
+    auto stage = [&](auto slot_c, uint32_t s) {
+        constexpr int S = decltype(slot_c)::value;
+#pragma unroll
+        for (int gg = 0; gg < 3; ++gg) {
+            __builtin_amdgcn_sched_barrier(0);
+            read_ops(S, gg + 1, (gg + 1) & 1);
+            mfma4(gg & 1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F78);   // vmcnt(8): stages s+2, s+3 may be in flight
+        lds_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        dma(S, min((s + 4) * BK, last_k0));
+        read_ops((S + 1) & 3, 0, 0);
+        mfma4(1);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+#pragma unroll
+    for (int st = 0; st < 4; ++st) dma(st, st * BK);
+    __builtin_amdgcn_s_waitcnt(0x0F7C);   // vmcnt(12): stage 0 has landed
+    lds_barrier();
+    read_ops(0, 0, 0);
+    // nstages % 4 == 0, so the body is straight-line; past the last stage the
+    // clamped DMAs re-read it into slots that are never read again.
+    for (uint32_t s = 0; s < nstages; s += 4) {
+        stage(std::integral_constant<int, 0>{}, s);
+        stage(std::integral_constant<int, 1>{}, s + 1);
+        stage(std::integral_constant<int, 2>{}, s + 2);
+        stage(std::integral_constant<int, 3>{}, s + 3);
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // no DMA may still target LDS
+    __syncthreads();
+
+    // The second K half hands its partial sums to the first through LDS.
+    float* red = &L[0][0];
+    if (wk == 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[((wave & 3) * 16 + r) * 64 + lane] = acc[r];
+    }
+    __syncthreads();
+    if (wk == 1) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] += red[((wave & 3) * 16 + r) * 64 + lane];
+
+    // 32x32 accumulator layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
+    const uint32_t gc = n0 + wn * 32 + li;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const uint32_t gr = m0 + wm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        C[(size_t)gr * g.ldc + gc] = acc[r];
+    }
+}
+
 template <int BL, int EPI, bool RMS>
 int launch_variant(const GemmF32Args& g, uint32_t batch, hipStream_t s) {
     const uint64_t nblocks = (uint64_t)cdiv(g.m, BM) * g.tiles_n;
@@ -282,6 +423,14 @@ int launch_variant(const GemmF32Args& g, uint32_t batch, hipStream_t s) {
                      (uint64_t)g.m * g.lda * 4 < 0x80000000ull &&
                      b_rows * g.ldb * 4 < 0x80000000ull;
     const dim3 grid((uint32_t)nblocks, batch), block(512);
+    // full tiles of the plain product (sqr_mm, rect_mm, batch_mm,
+    // fused_qkv_projection) take the DMA kernel
+    if (BL == BL_KN && !RMS && EPI == EPI_STORE && vec && g.m % BM == 0 && g.n % BN == 0 &&
+        g.k % (4 * BK) == 0 && g.k > 0) {
+        hipLaunchKernelGGL(gemm_f32_dma_kernel, grid, block, 0, s, g);
+        MB_LAUNCH_CHECK("matmul_f32");
+        return MB_OK;
+    }
     if (vec) hipLaunchKernelGGL((gemm_f32_kernel<2, true, BL, EPI, RMS>), grid, block, 0, s, g);
     else hipLaunchKernelGGL((gemm_f32_kernel<2, false, BL, EPI, RMS>), grid, block, 0, s, g);
     MB_LAUNCH_CHECK("matmul_f32");

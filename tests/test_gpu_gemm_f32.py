@@ -15,6 +15,8 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize("m,n,k", [
     (1, 1, 1), (1, 64, 64), (64, 1, 64), (64, 64, 1), (64, 64, 64), (65, 33, 17),
     (128, 256, 64), (100, 300, 96), (257, 129, 200), (512, 512, 512), (31, 1000, 36),
+    # full tiles with K % 256 == 0 take the LDS-DMA kernel: one loop trip, three trips
+    (64, 64, 256), (192, 128, 768),
 ])
 def test_matmul_f32_shapes(mb, dev, m, n, k):
     a = seeded(m * 1000 + k, (m, k), ("uniform", -1.0, 1.0))
@@ -33,12 +35,13 @@ def test_matmul_f32_k0_gives_zeros(mb, dev):
     assert torch.all(d_c.cpu() == 0.0)
 
 
-def test_matmul_f32_identity_exact(mb, dev):
-    a = seeded(3, (192, 192))
-    eye = torch.eye(192)
+@pytest.mark.parametrize("n", [192, 256])   # register-staged kernel, LDS-DMA kernel
+def test_matmul_f32_identity_exact(mb, dev, n):
+    a = seeded(3, (n, n))
+    eye = torch.eye(n)
     d_a, d_eye = a.to(dev), eye.to(dev)     # keep both alive across the launch
-    d_c = torch.zeros((192, 192), device=dev)
-    launch("mb_launch_matmul_f32", ptr(d_a), ptr(d_eye), ptr(d_c), 192, 192, 192, None)
+    d_c = torch.zeros((n, n), device=dev)
+    launch("mb_launch_matmul_f32", ptr(d_a), ptr(d_eye), ptr(d_c), n, n, n, None)
     assert torch.equal(d_c.cpu(), a)
 
 
