@@ -11,21 +11,21 @@
 //   B[k][o] = w[o][k]                                    (OHWI rows are K-contiguous)
 // and y[m][o] is exactly the NHWC output.
 //
-// gfx950 design:
-//  * workgroup tile 64 pixels x 64 channels, BK = 32; 4 waves each own a 32x32
-//    sub-tile (v_mfma_f32_32x32x2f32); KSPLIT = 2 doubles the waves (two per
-//    SIMD), the second set taking the other half of each stage's K range;
-//  * both operands are staged K-contiguous in LDS (row stride 36 floats: 16
-//    lanes reading 16 consecutive rows with ds_read_b128 cover all 64 banks
-//    once), so one ds_read_b128 per operand feeds four MFMAs;
-//  * fast path (C % 32 == 0): a BK = 32 stage never straddles a filter tap
-//    (r, s), so the tap is uniform per stage and each A row is one contiguous
-//    128-byte NHWC channel run, loaded as float4 or zero-filled at the image
-//    border.  The per-row (n, p, q) decomposition is hoisted out of the K loop
-//    (the reference kernel hoists its im2col math the same way,
-//    metal/kernels/common/conv2d/default.metal:80-89);
-//  * any other shape takes the generic path: element-wise gathers with the
-//    (r, s, c) decomposition per element.
+// gfx950 design (v_mfma_f32_32x32x2f32 on 32x32 sub-tiles; two K halves per
+// stage on separate waves, summed through LDS at the end):
+//  * fast path (C % 32 == 0, conv2d_f32_dma_kernel): a BK = 32 stage never
+//    straddles a filter tap (r, s), so the tap is uniform per stage and each
+//    A row is one contiguous 128-byte NHWC channel run, fetched by DMA
+//    straight into LDS or zero-filled at the image border.  The per-row
+//    (n, p, q) decomposition is hoisted out of the K loop (the reference
+//    kernel hoists its im2col math the same way,
+//    metal/kernels/common/conv2d/default.metal:80-89).  Tiles are 32 pixels
+//    x 64 channels (details at the kernel);
+//  * any other shape (conv2d_f32_kernel): 64 x 64 tiles with 8 waves, both
+//    operands gathered element-wise, staged two stages ahead in registers
+//    and stored K-contiguous in LDS (row stride 36 floats: 16 lanes reading
+//    16 consecutive rows with ds_read_b128 cover all 64 banks once), so one
+//    ds_read_b128 per operand feeds four MFMAs.
 #include "common.h"
 
 namespace mb {
@@ -43,7 +43,7 @@ struct ConvShape {
     uint32_t k;   // r*s*c
 };
 
-template <int KSPLIT, bool FAST>
+template <int KSPLIT>
 __global__ __launch_bounds__(256 * KSPLIT)
 void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt,
                        float* __restrict__ Y, ConvShape sh, uint32_t tiles_n) {
@@ -82,68 +82,37 @@ void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt
         row_base[i] = (uint64_t)nn * sh.h * sh.w * sh.c;
     }
 
-    // Two register stages (see the stage loop below).  FAST loads are buffer
-    // loads: taps outside the image and k past the filter read zeros through
-    // an out-of-range offset, so the loads carry no branches.
+    // Two register stages (see the stage loop below); element-wise gathers.
     float4 ra[2][LOADS], rb[2][LOADS];
-    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(X), 0, sh.n * sh.h * sh.w * sh.c * 4, 0x00020000u);
-    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(Wt), 0, sh.o * sh.k * 4, 0x00020000u);
-    auto ld4 = [](__amdgpu_buffer_rsrc_t rsrc, uint32_t off) {
-        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
-    };
     auto load = [&](int set, uint32_t k0) {
-        if (FAST) {
-            // Uniform tap for the stage: k0 = (r*S + s)*C + c0 (k0 past the filter
-            // gives r >= R, which the row test below turns into zeros).
-            const uint32_t rs = k0 / sh.c, c0 = k0 - rs * sh.c;
-            const uint32_t r = rs / sh.s, s = rs - r * sh.s;
 #pragma unroll
-            for (int i = 0; i < LOADS; ++i) {
-                const uint32_t q4 = ((tid + i * NT) % KQ) * 4;
-                const int32_t hi = row_h0[i] + (int32_t)r, wi = row_w0[i] + (int32_t)s;
-                const bool in = row_ok[i] && k0 < sh.k && hi >= 0 && hi < (int32_t)sh.h &&
-                                wi >= 0 && wi < (int32_t)sh.w;
-                const uint32_t off =
-                    in ? ((uint32_t)row_base[i] + ((uint32_t)hi * sh.w + wi) * sh.c + c0 + q4) * 4
-                       : 0x80000000u;
-                ra[set][i] = ld4(xrs, off);
-            }
-        } else {
+        for (int i = 0; i < LOADS; ++i) {
+            const uint32_t q4 = ((tid + i * NT) % KQ) * 4;
+            float v[4];
 #pragma unroll
-            for (int i = 0; i < LOADS; ++i) {
-                const uint32_t q4 = ((tid + i * NT) % KQ) * 4;
-                float v[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t kk = k0 + q4 + e;
-                    v[e] = 0.f;
-                    if (row_ok[i] && kk < sh.k) {
-                        const uint32_t rs = kk / sh.c, c = kk - rs * sh.c;
-                        const uint32_t r = rs / sh.s, s = rs - r * sh.s;
-                        const int32_t hi = row_h0[i] + (int32_t)r, wi = row_w0[i] + (int32_t)s;
-                        if (hi >= 0 && hi < (int32_t)sh.h && wi >= 0 && wi < (int32_t)sh.w)
-                            v[e] = X[row_base[i] + ((uint64_t)hi * sh.w + wi) * sh.c + c];
-                    }
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t kk = k0 + q4 + e;
+                v[e] = 0.f;
+                if (row_ok[i] && kk < sh.k) {
+                    const uint32_t rs = kk / sh.c, c = kk - rs * sh.c;
+                    const uint32_t r = rs / sh.s, s = rs - r * sh.s;
+                    const int32_t hi = row_h0[i] + (int32_t)r, wi = row_w0[i] + (int32_t)s;
+                    if (hi >= 0 && hi < (int32_t)sh.h && wi >= 0 && wi < (int32_t)sh.w)
+                        v[e] = X[row_base[i] + ((uint64_t)hi * sh.w + wi) * sh.c + c];
                 }
-                ra[set][i] = make_float4(v[0], v[1], v[2], v[3]);
             }
+            ra[set][i] = make_float4(v[0], v[1], v[2], v[3]);
         }
         // B tile: 64 output channels x 32 k, rows of w are K-contiguous.
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             const uint32_t q = tid + i * NT;
             const uint32_t oc = n0 + q / KQ, kq = k0 + (q % KQ) * 4;
-            if (FAST) {
-                rb[set][i] = ld4(wrs, (oc < sh.o && kq < sh.k) ? (oc * sh.k + kq) * 4 : 0x80000000u);
-            } else {
-                float v[4];
+            float v[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    v[e] = (oc < sh.o && kq + e < sh.k) ? Wt[(uint64_t)oc * sh.k + kq + e] : 0.f;
-                rb[set][i] = make_float4(v[0], v[1], v[2], v[3]);
-            }
+            for (int e = 0; e < 4; ++e)
+                v[e] = (oc < sh.o && kq + e < sh.k) ? Wt[(uint64_t)oc * sh.k + kq + e] : 0.f;
+            rb[set][i] = make_float4(v[0], v[1], v[2], v[3]);
         }
     };
     auto store = [&](int set, int buf) {
@@ -157,12 +126,9 @@ void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt
 
     f32x16 acc = {};
     const uint32_t li = lane & 31, lh = lane >> 5;
-    // FAST: an even number of stages and no branch in the loop body (a stage
-    // past K multiplies the zeros its out-of-range loads stored).
-    const uint32_t nrun = FAST ? (nstages + 1) & ~1u : nstages;
     if (nstages > 0) {
         load(0, 0);
-        if (FAST || nstages > 1) load(1, BK);
+        if (nstages > 1) load(1, BK);
         store(0, 0);
         __syncthreads();
     }
@@ -171,7 +137,7 @@ void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt
     // registers go to LDS in the middle of stage st's MFMAs.  The operands of
     // group g+1 are read from LDS while group g's MFMAs run.
     auto stage = [&](uint32_t st, int cur) {
-        if (FAST || st + 2 < nstages) load(cur, (st + 2) * BK);
+        if (st + 2 < nstages) load(cur, (st + 2) * BK);
         __builtin_amdgcn_sched_barrier(0);
         const float* as = &As[cur][(wm * 32 + li) * SK + 4 * lh];
         const float* bs = &Bs[cur][(wn * 32 + li) * SK + 4 * lh];
@@ -187,7 +153,7 @@ void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt
         for (int gg = 0; gg < NG; ++gg) {
             __builtin_amdgcn_sched_barrier(0);
             if (gg + 1 < NG) read_ops(gg + 1, (gg + 1) & 1);
-            if (gg == NG / 2 && (FAST || st + 1 < nstages)) store(cur ^ 1, cur ^ 1);
+            if (gg == NG / 2 && st + 1 < nstages) store(cur ^ 1, cur ^ 1);
             __builtin_amdgcn_sched_barrier(0);
             const int sl = gg & 1;
             acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[sl].x, b4[sl].x, acc, 0, 0, 0);
@@ -198,9 +164,9 @@ void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
     };
-    for (uint32_t st = 0; st < nrun; st += 2) {
+    for (uint32_t st = 0; st < nstages; st += 2) {
         stage(st, 0);
-        if (FAST || st + 1 < nstages) stage(st + 1, 1);
+        if (st + 1 < nstages) stage(st + 1, 1);
     }
 
     if (KSPLIT == 2) {
@@ -214,6 +180,167 @@ void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r] += red[((wave & 3) * 16 + r) * 64 + lane];
     }
+
+    // 32x32 accumulator: lane l, reg r -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
+    const uint32_t gc = n0 + wn * 32 + li;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const uint32_t gr = m0 + wm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (gr < sh.m && gc < sh.o) Y[(uint64_t)gr * sh.o + gc] = acc[r];
+    }
+}
+
+// Fast-path kernel (C % 32 == 0): the operands go global -> LDS by DMA
+// (buffer_load ... lds) into a ring of NBUF = 2 32-deep k stages: no staging
+// registers and no LDS store instructions, whose VGPR reads stall the MFMA
+// issue.  A tile is 32 WMS pixels x 64 channels with 4 WMS waves (K halves x
+// row groups x column halves, v_mfma_f32_32x32x2f32 on 32x32 sub-tiles, the
+// K halves summed through LDS).  The launcher uses WMS = 1: 32-pixel tiles,
+// 12 KB per ring slot, six workgroups per CU, so the 3136 tiles of the
+// 32x56x56 shape finish in finer rounds than 64-pixel tiles would.
+//  * a slot holds BMT A rows (output pixels: one NHWC channel run of the
+//    stage's tap) and 64 B rows (output channels: OHWI weight rows are
+//    K-contiguous), each 32 k = 128 bytes; 16-byte chunk c of row r sits in
+//    slot c ^ ((r / 2) % 8), so a ds_read_b128 of 16 consecutive rows touches
+//    16 distinct bank groups 8 (r % 2) + slot;
+//  * a DMA instruction writes a wave's 64 x 16 B = eight rows contiguously;
+//    wave w fetches A rows 8 w .. 8 w + 7 and 8 x BI B rows, lane l the chunk
+//    that slot l % 8 of its row holds.  Taps outside the image and k past the
+//    filter use an out-of-range offset, which the DMA lands as zeros;
+//  * stage s (slot s % NBUF): group 0 reads group 1's operands under its 4
+//    MFMAs; before group 1 the wave waits for its DMAs of stage s+1, passes an
+//    LDS barrier, refills slot s % NBUF with stage s+NBUF and reads stage
+//    s+1's first operands under group 1's MFMAs.
+// Measured on the 32x56x56x64 -> 64 shape, alternated on one box: 90.2-91.3
+// us against 95.2-96.1 us for the register-staged version of this path
+// (conv2d_f32_kernel's layout with buffer loads); 64-pixel tiles (WMS = 2)
+// 91.5-92.5 us; a ring of three or four stages was slower (fewer workgroups
+// per CU).
+constexpr int NBUF = 2;
+
+// WMS = 32-pixel row groups per tile (tile BMT = 32 WMS pixels x 64 channels,
+// 4 WMS waves).
+template <int WMS>
+__global__ __launch_bounds__(256 * WMS)
+void conv2d_f32_dma_kernel(const float* __restrict__ X, const float* __restrict__ Wt,
+                           float* __restrict__ Y, ConvShape sh, uint32_t tiles_n) {
+    constexpr int BMT = 32 * WMS, NW = 4 * WMS;
+    constexpr int A_BYTES = BMT * BK * 4, C_SLOT = (BMT + BN) * BK;   // floats per ring slot
+    constexpr int BI = 2 / WMS;            // B DMA instructions per wave per stage
+    constexpr int D = 1 + BI;              // DMA instructions per wave per stage
+    __shared__ __attribute__((aligned(1024))) float L[NBUF * C_SLOT];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wk = wave / (2 * WMS), wm = (wave >> 1) % WMS, wn = wave & 1;
+    const uint32_t tm = blockIdx.x / tiles_n;
+    const uint32_t tn = blockIdx.x - tm * tiles_n;
+    const uint32_t m0 = tm * BMT, n0 = tn * BN;
+    const uint32_t nstages = (sh.k + BK - 1) / BK;
+    const uint32_t nrun = (nstages + 1) & ~1u;
+
+    const i32x4 xrs = dma_rsrc(X, sh.n * sh.h * sh.w * sh.c * 4);
+    const i32x4 wrs = dma_rsrc(Wt, sh.o * sh.k * 4);
+    // This lane's DMA row (8 w + l/8) and chunk; the pixel's image base and
+    // top-left tap are hoisted out of the K loop.
+    const uint32_t drow = 8 * wave + (lane >> 3);
+    const uint32_t dch = (lane & 7) ^ ((drow >> 1) & 7);
+    const uint32_t m = m0 + drow;
+    const bool m_ok = m < sh.m;
+    const uint32_t mm = m_ok ? m : 0;
+    const uint32_t qq = mm % sh.q, t = mm / sh.q;
+    const uint32_t pp = t % sh.p, nn = t / sh.p;
+    const int32_t h0 = (int32_t)(pp * sh.stride) - (int32_t)sh.pad;
+    const int32_t w0 = (int32_t)(qq * sh.stride) - (int32_t)sh.pad;
+    const uint32_t xbase = nn * sh.h * sh.w * sh.c + 4 * dch;
+    // B rows (output channels) of this wave: BI instructions of 8 rows each
+    uint32_t oc[BI], bch[BI];
+    bool o_ok[BI];
+#pragma unroll
+    for (int i = 0; i < BI; ++i) {
+        const uint32_t brow = 8 * (BI * wave + i) + (lane >> 3);
+        bch[i] = (lane & 7) ^ ((brow >> 1) & 7);
+        oc[i] = n0 + brow;
+        o_ok[i] = oc[i] < sh.o;
+    }
+    const uint32_t l0 = lds_addr(L);
+    const uint32_t dst = 8 * wave * 128;   // this wave's A rows in a slot
+    auto dma = [&](uint32_t slot, uint32_t k0) {
+        // uniform tap of the stage: k0 = (r*S + s)*C + c0 (k0 past the filter
+        // reads as an image miss)
+        const uint32_t rs = k0 / sh.c, c0 = k0 - rs * sh.c;
+        const uint32_t r = rs / sh.s, s = rs - r * sh.s;
+        const int32_t hi = h0 + (int32_t)r, wi = w0 + (int32_t)s;
+        const bool in = m_ok && k0 < sh.k && hi >= 0 && hi < (int32_t)sh.h && wi >= 0 &&
+                        wi < (int32_t)sh.w;
+        const uint32_t xo = in ? (xbase + ((uint32_t)hi * sh.w + wi) * sh.c + c0) * 4 : 0x80000000u;
+        dma16(xrs, l0 + slot * (C_SLOT * 4) + dst, xo, 0);
+#pragma unroll
+        for (int i = 0; i < BI; ++i) {
+            const uint32_t wo =
+                (o_ok[i] && k0 < sh.k) ? (oc[i] * sh.k + k0 + 4 * bch[i]) * 4 : 0x80000000u;
+            dma16(wrs, l0 + slot * (C_SLOT * 4) + A_BYTES + 8 * (BI * wave + i) * 128, wo, 0);
+        }
+    };
+
+    const uint32_t li = lane & 31, lh = lane >> 5;
+    // operand of group g (8 k): row wm*32 + li (A) / wn*32 + li (B), chunk
+    // 2 g + lh, in slot chunk ^ ((li/2) % 8)
+    const uint32_t a_row = (wm * 32 + li) * 128, b_row = A_BYTES + (wn * 32 + li) * 128;
+    const uint32_t sw = (li >> 1) & 7;
+    const uint8_t* l8 = reinterpret_cast<const uint8_t*>(L);
+    float4 a4[2], b4[2];
+    auto read_ops = [&](uint32_t slot, int gg, int c) {
+        const uint32_t g = 2 * wk + gg;
+        const uint8_t* base = l8 + slot * (C_SLOT * 4) + 16 * ((2 * g + lh) ^ sw);
+        a4[c] = *reinterpret_cast<const float4*>(base + a_row);
+        b4[c] = *reinterpret_cast<const float4*>(base + b_row);
+    };
+    f32x16 acc = {};
+    auto mfma4 = [&](int c) {
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[c].x, b4[c].x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[c].y, b4[c].y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[c].z, b4[c].z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[c].w, b4[c].w, acc, 0, 0, 0);
+    };
+
+#pragma unroll
+    for (uint32_t st = 0; st < NBUF; ++st) dma(st, st * BK);
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (D * (NBUF - 1)));   // stage 0 has landed
+    lds_barrier();
+    read_ops(0, 0, 0);
+    // nrun is even and stages past K multiply zeros; DMAs past the last stage
+    // land as zeros in slots that are never read again.
+    uint32_t slot = 0;
+    for (uint32_t st = 0; st < nrun; ++st) {
+        const uint32_t nslot = slot + 1 == NBUF ? 0 : slot + 1;
+        __builtin_amdgcn_sched_barrier(0);
+        read_ops(slot, 1, 1);
+        mfma4(0);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (D * (NBUF - 2)));   // stage st+1 has landed
+        lds_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        dma(slot, (st + NBUF) * BK);
+        read_ops(nslot, 0, 0);
+        mfma4(1);
+        __builtin_amdgcn_sched_barrier(0);
+        slot = nslot;
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // no DMA may still target LDS
+    lds_barrier();
+
+    float* red = L;   // NW/2 waves x 16 x 64 floats
+    const uint32_t rw = wave % (NW / 2);
+    if (wk == 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[(rw * 16 + r) * 64 + lane] = acc[r];
+    }
+    __syncthreads();
+    if (wk == 1) return;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] += red[(rw * 16 + r) * 64 + lane];
 
     // 32x32 accumulator: lane l, reg r -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
     const uint32_t gc = n0 + wn * 32 + li;
@@ -247,17 +374,20 @@ int launch_conv2d(const float* x, const float* w, float* y, uint32_t n, uint32_t
     const uint32_t tiles_m = cdiv(sh.m, BM), tiles_n = cdiv(o, BN);
     const uint64_t nblocks = (uint64_t)tiles_m * tiles_n;
     if (nblocks > 0x7fffffffull) return fail(MB_E_ARG, "conv2d_f32: shape too large");
-    // FAST: a stage never straddles a tap, 16-byte aligned rows, and buffer-load
+    // fast path: a stage never straddles a tap, 16-byte aligned rows, and DMA
     // offsets of both operands within 2 GB
     const bool fast = (c % BK == 0) && ((((uintptr_t)x) | ((uintptr_t)w)) & 15) == 0 &&
                       (uint64_t)n * h * wd * c * 4 < 0x80000000ull &&
                       (uint64_t)o * k * 4 < 0x80000000ull;
-    if (fast)
-        hipLaunchKernelGGL((conv2d_f32_kernel<2, true>), dim3((uint32_t)nblocks), dim3(512), 0, st,
+    if (fast) {
+        const uint64_t dma_blocks = (uint64_t)cdiv(sh.m, 32) * tiles_n;
+        if (dma_blocks > 0x7fffffffull) return fail(MB_E_ARG, "conv2d_f32: shape too large");
+        hipLaunchKernelGGL(conv2d_f32_dma_kernel<1>, dim3((uint32_t)dma_blocks), dim3(256), 0, st,
                            x, w, y, sh, tiles_n);
-    else
-        hipLaunchKernelGGL((conv2d_f32_kernel<2, false>), dim3((uint32_t)nblocks), dim3(512), 0, st,
+    } else {
+        hipLaunchKernelGGL((conv2d_f32_kernel<2>), dim3((uint32_t)nblocks), dim3(512), 0, st,
                            x, w, y, sh, tiles_n);
+    }
     MB_LAUNCH_CHECK("conv2d_f32");
     return MB_OK;
 }
@@ -290,7 +420,7 @@ int run_conv2d(const Bindings& bs, hipStream_t st, PartMarks*) {
 
 void register_conv2d() {
     register_kernel({"conv2d_f32", run_conv2d,
-                     reinterpret_cast<const void*>(&conv2d_f32_kernel<2, true>), 1});
+                     reinterpret_cast<const void*>(&conv2d_f32_dma_kernel<1>), 1});
 }
 
 }  // namespace mb

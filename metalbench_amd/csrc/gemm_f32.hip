@@ -305,7 +305,7 @@ void gemm_f32_dma_kernel(GemmF32Args g) {
     const uint32_t tn = blockIdx.x - tm * g.tiles_n;
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(tm * BM);
     const uint32_t n0 = __builtin_amdgcn_readfirstlane(tn * BN);
-    const uint32_t N = g.n, K = g.k, lda = g.lda, ldb = g.ldb;
+    const uint32_t K = g.k, lda = g.lda, ldb = g.ldb;
     const uint32_t nstages = K / BK;   // a multiple of 4
     const uint32_t last_k0 = K - BK;
     const float* A = g.a + (size_t)blockIdx.y * g.batch_a;
