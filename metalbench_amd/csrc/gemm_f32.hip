@@ -269,8 +269,9 @@ void gemm_f32_kernel(GemmF32Args g) {
     }
 }
 
-// Full-tile kernel for C = A B: M, N multiples of 64, K of 256, B [K][N],
-// 16-byte aligned rows, operands under 2 GB.  Same tile, waves and MFMA as
+// Full-tile kernel for C = A B: M, N multiples of 64, K a multiple of 256 and
+// at least 512, B [K][N], 16-byte aligned rows, operands under 2 GB.  Same
+// tile, waves and MFMA as
 // gemm_f32_kernel<2, true, BL_KN, EPI_STORE, false>, but the operands go
 // global -> LDS by DMA (buffer_load ... lds) into a ring of four 64-deep k
 // stages (A 16 KB + B 16 KB each): no staging registers and no LDS store
@@ -423,10 +424,12 @@ int launch_variant(const GemmF32Args& g, uint32_t batch, hipStream_t s) {
                      (uint64_t)g.m * g.lda * 4 < 0x80000000ull &&
                      b_rows * g.ldb * 4 < 0x80000000ull;
     const dim3 grid((uint32_t)nblocks, batch), block(512);
-    // full tiles of the plain product (sqr_mm, rect_mm, batch_mm,
-    // fused_qkv_projection) take the DMA kernel
+    // full tiles of the plain product (sqr_mm, rect_mm, fused_qkv_projection)
+    // take the DMA kernel when K is long enough for its ring to pay: at K = 256
+    // (batch_mm's 128 x (128x512x256)) its 128 KB of LDS (one workgroup per
+    // CU) made it 4-5 % slower than the register-staged kernel
     if (BL == BL_KN && !RMS && EPI == EPI_STORE && vec && g.m % BM == 0 && g.n % BN == 0 &&
-        g.k % (4 * BK) == 0 && g.k > 0) {
+        g.k % (4 * BK) == 0 && g.k >= 8 * BK) {
         hipLaunchKernelGGL(gemm_f32_dma_kernel, grid, block, 0, s, g);
         MB_LAUNCH_CHECK("matmul_f32");
         return MB_OK;

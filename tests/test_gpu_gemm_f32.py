@@ -15,8 +15,9 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize("m,n,k", [
     (1, 1, 1), (1, 64, 64), (64, 1, 64), (64, 64, 1), (64, 64, 64), (65, 33, 17),
     (128, 256, 64), (100, 300, 96), (257, 129, 200), (512, 512, 512), (31, 1000, 36),
-    # full tiles with K % 256 == 0 take the LDS-DMA kernel: one loop trip, three trips
-    (64, 64, 256), (192, 128, 768),
+    # full tiles with K % 256 == 0 and K >= 512 take the LDS-DMA kernel: two loop
+    # trips, three trips
+    (64, 64, 512), (192, 128, 768),
 ])
 def test_matmul_f32_shapes(mb, dev, m, n, k):
     a = seeded(m * 1000 + k, (m, k), ("uniform", -1.0, 1.0))

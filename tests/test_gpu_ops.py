@@ -102,7 +102,7 @@ def test_swiglu_shapes(mb, m, n, k):
     assert_close(f64(y), oracle.swiglu(f64(x), f64(wg), f64(wu)), 1e-3, 1e-3, f"swiglu {m,n,k}")
 
 
-@pytest.mark.parametrize("batch,m,n,k", [(3, 70, 50, 33), (2, 64, 128, 256)])
+@pytest.mark.parametrize("batch,m,n,k", [(3, 70, 50, 33), (2, 64, 128, 256), (2, 64, 128, 512)])
 def test_batch_mm_shapes(mb, batch, m, n, k):
     a, b = seeded(9, (batch, m, k)), seeded(10, (batch, k, n))
     (c,) = run_bound("batch_matmul_f32", [(0, a), (1, b)], [(2, (batch, m, n))],
