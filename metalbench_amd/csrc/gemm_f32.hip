@@ -560,10 +560,13 @@ int run_swiglu(const Bindings& bs, hipStream_t s, PartMarks*) {
 void register_gemm_f32() {
     const void* plain = reinterpret_cast<const void*>(
         &gemm_f32_kernel<2, true, BL_KN, EPI_STORE, false>);
-    // sqr_mm, rect_mm and fused_qkv_projection share the plain GEMM's spec.
-    register_kernel({"sqr_matmul_f32", run_gemm_f32, plain, 1});
-    register_kernel({"rect_matmul_f32", run_gemm_f32, plain, 1});
-    register_kernel({"fused_qkv_projection_f32", run_gemm_f32, plain, 1});
+    // sqr_mm, rect_mm and fused_qkv_projection share the plain GEMM's spec;
+    // their registry shapes run the LDS-DMA kernel, whose attributes (LDS
+    // size, threads) the report prints.
+    const void* dma = reinterpret_cast<const void*>(&gemm_f32_dma_kernel);
+    register_kernel({"sqr_matmul_f32", run_gemm_f32, dma, 1});
+    register_kernel({"rect_matmul_f32", run_gemm_f32, dma, 1});
+    register_kernel({"fused_qkv_projection_f32", run_gemm_f32, dma, 1});
     register_kernel({"batch_matmul_f32", run_batch_mm, plain, 1});
     register_kernel({"rms_norm_linear_f32", run_rms_norm_linear,
                      reinterpret_cast<const void*>(&gemm_f32_kernel<2, true, BL_NK, EPI_STORE, true>),
