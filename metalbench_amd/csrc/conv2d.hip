@@ -238,7 +238,6 @@ void conv2d_f32_dma_kernel(const float* __restrict__ X, const float* __restrict_
     const uint32_t tn = blockIdx.x - tm * tiles_n;
     const uint32_t m0 = tm * BMT, n0 = tn * BN;
     const uint32_t nstages = (sh.k + BK - 1) / BK;
-    const uint32_t nrun = (nstages + 1) & ~1u;
 
     const i32x4 xrs = dma_rsrc(X, sh.n * sh.h * sh.w * sh.c * 4);
     const i32x4 wrs = dma_rsrc(Wt, sh.o * sh.k * 4);
@@ -310,10 +309,9 @@ void conv2d_f32_dma_kernel(const float* __restrict__ X, const float* __restrict_
     __builtin_amdgcn_s_waitcnt(0x0F70 | (D * (NBUF - 1)));   // stage 0 has landed
     lds_barrier();
     read_ops(0, 0, 0);
-    // nrun is even and stages past K multiply zeros; DMAs past the last stage
-    // land as zeros in slots that are never read again.
+    // DMAs past the last stage land as zeros in slots that are never read.
     uint32_t slot = 0;
-    for (uint32_t st = 0; st < nrun; ++st) {
+    for (uint32_t st = 0; st < nstages; ++st) {
         const uint32_t nslot = slot + 1 == NBUF ? 0 : slot + 1;
         __builtin_amdgcn_sched_barrier(0);
         read_ops(slot, 1, 1);
