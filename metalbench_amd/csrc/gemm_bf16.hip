@@ -343,12 +343,16 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
 #pragma unroll
         for (int i = 1; i < 4; ++i) a[c][i] = a_at(i);
     };
+    // Snake order over j (odd i run j backwards), so consecutive MFMAs always
+    // share an operand register: 0.3-0.5 % faster at the power-limited clock.
     auto mfmas = [&](int c) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int jj = 0; jj < 4; ++jj) {
+                const int j = (i & 1) ? 3 - jj : jj;
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[c][i], b[c][j], acc[i][j], 0, 0, 0);
+            }
     };
     // One stage on ring buffer rc (pointer cur); `kdma` is the k of the stage
     // that refills it.  k step 1 is four chunks, each: two DMAs, three
@@ -378,8 +382,10 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
             a[0][q] = *reinterpret_cast<const bf16x8*>(nas + 32 * q * AROWB + 16 * (lh ^ a_sw));
             b[0][q] = b_at(nbs, q, 0);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int jj = 0; jj < 4; ++jj) {
+                const int j = (q & 1) ? 3 - jj : jj;
                 acc[q][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][q], b[1][j], acc[q][j], 0, 0, 0);
+            }
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
             __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // DS read
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
