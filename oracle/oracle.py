@@ -22,8 +22,13 @@ How each function is pinned (tests/test_oracle.py):
   gqa_decode_attention single key -> v, equal keys -> mean(v), G=1 == brute-force
                        MHA, head h reads kv head h // G (distinct-valued heads)
   silu / swiglu        silu(0) = 0, scipy.special.expit form
-  llama_decoder_step   zero weights -> y = x; L = 0 equals the S = 1 prefill
-  llama_decoder_layer  zero weights -> y = x; S = 1 reduces to v @ W_o path
+  llama_decoder_step   pure-Python loops (math only) over the whole step with
+                       every weight non-zero; W_o = 0 -> y = x + FFN(x) by
+                       loops; zero weights -> y = x; L = 0 equals the S = 1
+                       prefill; planted FFN/residual/RoPE mutations fail
+  llama_decoder_layer  pure-Python loops over the whole layer; W_qkv = 0 ->
+                       y = x + FFN(x) by loops; zero weights -> y = x;
+                       planted FFN/residual mutations fail
   fused_add_rms_norm   residual 0 -> rms_norm(x); x = -residual -> 0
   rms_norm_linear      W = I -> rms_norm(x); brute-force loops
   swiglu               zero gate or up weights -> 0; brute-force loops

@@ -7,6 +7,9 @@ that do not restate its own formula: brute-force loops, a library routine
 and invariants, chosen so that a dropped term, a wrong sign/index or a
 transposed operand fails at least one of them.  A deliberately broken variant
 of the oracle is shown to fail these checks (planted mistakes, end of file)."""
+import inspect
+import math
+
 import numpy as np
 import pytest
 import scipy.special
@@ -259,6 +262,120 @@ def test_decoder_layer_zero_weights_is_identity():
     assert np.array_equal(y, x)
 
 
+# ---- the FFN half and the whole decoder against pure-Python loops --------------------------
+# Written from reference mlx/kernels/full/llama_decoder_layer.py:24-64 with
+# `math` only: h = rmsnorm(x) (:48-50); q|k|v = h W_qkv, columns [Q | K | V];
+# RoPE on pairs (2i, 2i+1) at angle pos * base^(-2i/Dh) (:52-64); query head h
+# reads kv head h // G (:34); softmax(q k / sqrt(Dh)) v; x1 = x + attn W_o;
+# h2 = rmsnorm(x1); y = x1 + (silu(h2 W_gate) * h2 W_up) W_down, W_gu columns
+# [gate | up] (:41-46), silu(v) = v / (1 + e^-v).
+
+def _rot(vec, pos, base):
+    out = list(vec)
+    for i in range(len(vec) // 2):
+        a = pos / base ** (2.0 * i / len(vec))
+        out[2 * i] = vec[2 * i] * math.cos(a) - vec[2 * i + 1] * math.sin(a)
+        out[2 * i + 1] = vec[2 * i] * math.sin(a) + vec[2 * i + 1] * math.cos(a)
+    return out
+
+
+def _loop_ffn(x1, w_gu, w_down, eps):
+    """Rows of x1 (the attention half's output) through the FFN half."""
+    d, ff = len(x1[0]), len(w_down)
+    out = []
+    for row in x1:
+        h2 = _brute_rms_row(list(row), eps)
+        act = []
+        for f in range(ff):
+            g = sum(h2[k] * w_gu[k][f] for k in range(d))
+            u = sum(h2[k] * w_gu[k][ff + f] for k in range(d))
+            act.append(g / (1.0 + math.exp(-g)) * u)
+        out.append([row[j] + sum(act[f] * w_down[f][j] for f in range(ff)) for j in range(d)])
+    return np.array(out)
+
+
+def _loop_decoder_step(x, w_qkv, w_o, w_gu, w_down, k_cache, v_cache, H, HKV, base, eps):
+    """One new token per sequence at position L attending to the L cached
+    (already rotated) keys and itself."""
+    B, D = x.shape
+    dh, g, L = D // H, H // HKV, k_cache.shape[2]
+    x1, k_new, v_new = [], np.zeros((B, HKV, dh)), np.zeros((B, HKV, dh))
+    for b in range(B):
+        h = _brute_rms_row(list(x[b]), eps)
+        qkv = [sum(h[k] * w_qkv[k, j] for k in range(D)) for j in range(w_qkv.shape[1])]
+        for kvh in range(HKV):
+            k_new[b, kvh] = _rot(qkv[D + kvh * dh:D + (kvh + 1) * dh], L, base)
+            v_new[b, kvh] = qkv[D + (HKV + kvh) * dh:D + (HKV + kvh + 1) * dh]
+        att = [0.0] * D
+        for hh in range(H):
+            kvh = hh // g
+            q = _rot(qkv[hh * dh:(hh + 1) * dh], L, base)
+            keys = [list(k_cache[b, kvh, j]) for j in range(L)] + [list(k_new[b, kvh])]
+            vals = [list(v_cache[b, kvh, j]) for j in range(L)] + [list(v_new[b, kvh])]
+            sc = [sum(qi * ki for qi, ki in zip(q, key)) / math.sqrt(dh) for key in keys]
+            mx = max(sc)
+            e = [math.exp(s - mx) for s in sc]
+            z = sum(e)
+            for dd in range(dh):
+                att[hh * dh + dd] = sum(e[j] / z * vals[j][dd] for j in range(L + 1))
+        x1.append([x[b, j] + sum(att[k] * w_o[k, j] for k in range(D)) for j in range(D)])
+    return _loop_ffn(x1, w_gu, w_down, eps), k_new, v_new
+
+
+def _step_inputs(seed=7, B=2, D=16, H=4, HKV=2, FF=6, L=3, scale=0.4):
+    r = np.random.default_rng(seed)
+    dh = D // H
+    n = lambda *s: r.standard_normal(s)  # noqa: E731
+    return dict(x=n(B, D), w_qkv=n(D, D + 2 * HKV * dh) * scale, w_o=n(D, D) * scale,
+                w_gu=n(D, 2 * FF) * scale, w_down=n(FF, D) * scale,
+                k_cache=n(B, HKV, L, dh), v_cache=n(B, HKV, L, dh))
+
+
+def _step_matches_loops(step_fn, a, H=4, HKV=2, base=500000.0, eps=1e-5):
+    y, kn, vn = step_fn(**a, n_heads=H, n_kv_heads=HKV, base=base, eps=eps)
+    wy, wk, wv = _loop_decoder_step(*(a[k] for k in ("x", "w_qkv", "w_o", "w_gu", "w_down",
+                                                     "k_cache", "v_cache")), H, HKV, base, eps)
+    return (np.allclose(y, wy, rtol=1e-10, atol=1e-10) and np.allclose(kn, wk, rtol=1e-10, atol=1e-10)
+            and np.allclose(vn, wv, rtol=1e-10, atol=1e-10))
+
+
+def _layer_matches_loops(layer_fn, x, wqkv, wo, wgu, wd, H=4, HKV=2, base=100.0, eps=1e-5):
+    got = layer_fn(x, wqkv, wo, wgu, wd, n_heads=H, n_kv_heads=HKV, base=base, eps=eps)
+    h = np.array([_brute_rms_row(list(row), eps) for row in x])
+    x1 = x + _brute_attention(h, wqkv, wo, H, HKV, base)
+    return np.allclose(got, _loop_ffn(x1, wgu, wd, eps), rtol=1e-10, atol=1e-10)
+
+
+def test_decoder_step_matches_loops():
+    # every weight non-zero, big enough that silu, softmax and RoPE are far from linear
+    assert _step_matches_loops(oracle.llama_decoder_step, _step_inputs())
+    assert _step_matches_loops(oracle.llama_decoder_step, _step_inputs(seed=8, H=4, HKV=1, L=5),
+                               HKV=1, base=10000.0)
+
+
+def test_decoder_step_ffn_half_with_zero_w_o():
+    # W_o = 0 makes x1 = x, so y is the FFN half of x alone; compared with loops
+    a = _decoder_inputs(2, 64, 4, 2, 96, 5, scale=0.2)
+    a["w_o"] = np.zeros_like(a["w_o"])
+    y, _, _ = oracle.llama_decoder_step(**a, n_heads=4, n_kv_heads=2)
+    assert np.allclose(y, _loop_ffn(a["x"], a["w_gu"], a["w_down"], 1e-5), rtol=1e-10, atol=1e-10)
+
+
+def test_decoder_layer_ffn_half_with_zero_w_qkv():
+    # W_qkv = 0 makes v = 0, hence attention = 0 and x1 = x
+    x, D, FF = rnd(5, 32), 32, 48
+    wgu, wd = rnd(D, 2 * FF) * 0.3, rnd(FF, D) * 0.3
+    y = oracle.llama_decoder_layer(x, np.zeros((D, 64)), rnd(D, D), wgu, wd, n_heads=4, n_kv_heads=2)
+    assert np.allclose(y, _loop_ffn(x, wgu, wd, 1e-5), rtol=1e-10, atol=1e-10)
+
+
+def test_decoder_layer_matches_loops():
+    S, D, H, HKV, FF = 3, 16, 4, 2, 6
+    x, wqkv, wo = rnd(S, D), rnd(D, D + 2 * HKV * (D // H)) * 0.4, rnd(D, D) * 0.4
+    wgu, wd = rnd(D, 2 * FF) * 0.4, rnd(FF, D) * 0.4
+    assert _layer_matches_loops(oracle.llama_decoder_layer, x, wqkv, wo, wgu, wd)
+
+
 # ---- decoder sub-ops at the reference shapes ---------------------------------------------
 
 def test_fused_add_rms_norm_closed_forms():
@@ -402,3 +519,49 @@ def test_planted_mistakes_are_caught(monkeypatch):
                                                    kn[:, [hh % hkv]], vn[:, [hh % hkv]])[0, 0, 0]
                        for hh in range(h)])
     assert not np.allclose(modulo, [hh // (h // hkv) + 1.0 for hh in range(h)])
+
+
+# Mutation checks: one plausible mistake planted in a copy of the oracle's own
+# source (exec'd in the oracle module's namespace) must fail the loop checks.
+def _mutant(fn, old, new):
+    src = inspect.getsource(fn)
+    assert src.count(old) == 1, f"mutation site {old!r} not found once in {fn.__name__}"
+    ns = dict(vars(oracle.oracle))
+    exec(compile(src.replace(old, new), "<mutant>", "exec"), ns)
+    return ns[fn.__name__]
+
+
+STEP_MUTATIONS = [
+    # gate and up halves swapped, i.e. silu on the up half
+    ("silu(gu[:, :ff_dim]) * gu[:, ff_dim:]", "silu(gu[:, ff_dim:]) * gu[:, :ff_dim]"),
+    ("silu(gu[:, :ff_dim]) * gu[:, ff_dim:]", "gu[:, :ff_dim] * gu[:, ff_dim:]"),         # no silu
+    ("silu(gu[:, :ff_dim]) * gu[:, ff_dim:]", "silu(gu[:, :ff_dim] * gu[:, ff_dim:])"),   # silu last
+    ("h2 = rms_norm(x1, eps)", "h2 = rms_norm(x, eps)"),          # FFN normalises x, not x1
+    ("y = x1 + act @", "y = x + act @"),                          # FFN residual from x
+    ("x1 = x + attn", "x1 = attn"),                               # attention residual dropped
+    ("q = rope_interleaved(q, pos, base)", "q = q"),              # q not rotated
+]
+
+
+@pytest.mark.parametrize("old,new", STEP_MUTATIONS)
+def test_planted_decoder_step_mistakes_are_caught(old, new):
+    assert not _step_matches_loops(_mutant(oracle.llama_decoder_step, old, new), _step_inputs())
+
+
+LAYER_MUTATIONS = [
+    ("(silu(gu[:, :ff_dim]) * gu[:, ff_dim:])", "(silu(gu[:, ff_dim:]) * gu[:, :ff_dim])"),
+    ("(silu(gu[:, :ff_dim]) * gu[:, ff_dim:])", "(gu[:, :ff_dim] * gu[:, ff_dim:])"),
+    ("h2 = rms_norm(x1, eps)", "h2 = rms_norm(x, eps)"),
+    ("return x1 + (", "return x + ("),
+]
+
+
+@pytest.mark.parametrize("old,new", LAYER_MUTATIONS)
+def test_planted_decoder_layer_mistakes_are_caught(old, new):
+    r = np.random.default_rng(3)
+    S, D, H, HKV, FF = 3, 16, 4, 2, 6
+    args = (r.standard_normal((S, D)), r.standard_normal((D, D + 2 * HKV * (D // H))) * 0.4,
+            r.standard_normal((D, D)) * 0.4, r.standard_normal((D, 2 * FF)) * 0.4,
+            r.standard_normal((FF, D)) * 0.4)
+    assert _layer_matches_loops(oracle.llama_decoder_layer, *args)
+    assert not _layer_matches_loops(_mutant(oracle.llama_decoder_layer, old, new), *args)
