@@ -22,8 +22,9 @@ multi-kernel step): `roofline.achieved` is the algorithmic bytes (HBM-bound
 kernels) or flops (MFMA-bound kernels) of ONE launch of the dominant kernel
 divided by that kernel's mean event-timed duration over those K steps.
 
-cpu_baseline: the float64 numpy oracle (oracle/), timed on this host on a
-bounded sample of the same workload — a reported baseline, not a target.
+cpu_baseline: the registry's torch-CPU Model spec (the harness's `mlx ref`
+line) timed on all host cores over the full workload -- a reported baseline,
+not a target.
 """
 from __future__ import annotations
 
@@ -128,84 +129,34 @@ def _traffic(key: str) -> float | None:
         return None
 
 
-def _blas_threads() -> int:
-    try:
-        from threadpoolctl import threadpool_info
-        n = [i.get("num_threads", 0) for i in threadpool_info() if i.get("user_api") == "blas"]
-        return max(n) if n else 1
-    except Exception:
-        return os.cpu_count() or 1
+def _cpu_baseline(name: str, b, inputs, meta: dict) -> dict:
+    """Time the registry's torch-CPU Model spec -- the same callable the
+    harness's `mlx ref` line times and the correctness gate compares against --
+    on the full workload, on every host core, with the statistics of reference
+    mlx/scripts/timing.py:31-72 (untimed warmup, then the median of the sorted
+    times), bounded to ~10-30 s of CPU work.  The spec computes at the
+    workload's precision: fp32 for the fp32 entries, the bf16 product with fp32
+    accumulation for large_mm, fp32 math on the bf16 weights and cache for the
+    decoder step (as the kernels do)."""
+    import platform
 
+    import torch
 
-def _cpu_baseline(name: str, inputs, meta: dict) -> dict:
-    """Time the float64 oracle on a bounded sample of the workload."""
-    import numpy as np
+    from metalbench_amd import helpers as H
+    from metalbench_amd.timing import time_cpu, use_all_cores
 
-    import oracle
-
-    f = oracle.as_f64
-
-    def timed(fn, budget_s=10.0, max_iters=5):
-        fn()   # warm
-        times = []
-        t_start = time.perf_counter()
-        while len(times) < max_iters and (time.perf_counter() - t_start) < budget_s:
-            t0 = time.perf_counter()
-            fn()
-            times.append(time.perf_counter() - t0)
-        times.sort()
-        return times[len(times) // 2], len(times)
-
-    if name == "llama_decoder_step":
-        args = [f(t) for t in inputs]
-        sec, n = timed(lambda: oracle.llama_decoder_step(*args, n_heads=_H, n_kv_heads=_HKV),
-                       budget_s=15.0, max_iters=3)
-        return {"value": sec * 1e6, "unit": "us/step", "cores": _blas_threads(), "kind": "port",
-                "sample": f"full decode step (B=16, L=2048) in float64 numpy, median of {n}"}
-    if name == "transpose_2d":
-        a = inputs[0].numpy()
-        sec, n = timed(lambda: oracle.transpose(a))
-        return {"value": meta["bytes"] / sec / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-                "sample": f"full 8192x8192 fp32 transpose (numpy copy), median of {n}"}
-    if name == "sqr_mm":
-        a, b = f(inputs[0]), f(inputs[1])
-        sec, n = timed(lambda: oracle.matmul(a, b))
-        return {"value": meta["flops"] / sec / 1e12, "unit": "TFLOP/s", "cores": _blas_threads(),
-                "kind": "port", "sample": f"full 1024^3 GEMM in float64 numpy, median of {n}"}
-    if name == "conv2d":
-        x, w = f(inputs[0]), f(inputs[1])
-        sec, n = timed(lambda: oracle.conv2d_nhwc(x, w, 1, 1), max_iters=3)
-        return {"value": meta["flops"] / sec / 1e12, "unit": "TFLOP/s", "cores": _blas_threads(),
-                "kind": "port", "sample": f"full conv2d in float64 numpy, median of {n}"}
-    generic = {   # the other registry entries: the full workload through its oracle
-        "rect_mm": lambda a: oracle.matmul(*a),
-        "batch_mm": lambda a: oracle.matmul(*a),
-        "matvec": lambda a: oracle.matmul(*a),
-        "fused_qkv_projection": lambda a: oracle.matmul(*a),
-        "rms_norm": lambda a: oracle.rms_norm(a[0], 1e-5),
-        "fused_add_rms_norm": lambda a: oracle.fused_add_rms_norm(a[0], a[1], 1e-5),
-        "rms_norm_linear": lambda a: oracle.rms_norm_linear(a[0], a[1], 1e-5),
-        "rope_embedding": lambda a: oracle.rope_embedding(a[0], 10000.0),
-        "swiglu": lambda a: oracle.swiglu(*a),
-        "llama_attention": lambda a: oracle.llama_attention(*a, n_heads=4, n_kv_heads=2),
-        "llama_decoder_layer": lambda a: oracle.llama_decoder_layer(*a, n_heads=4, n_kv_heads=2),
-    }
-    if name in generic:
-        args = [f(t) for t in inputs]
-        sec, n = timed(lambda: generic[name](args), max_iters=5)
-        value, unit, _ = _value_unit(name, meta, sec * 1e3)
-        return {"value": value, "unit": unit, "cores": _blas_threads(), "kind": "port",
-                "sample": f"full workload in float64 numpy, median of {n}"}
-    if name == "large_mm":
-        rows = 512
-        a = f(inputs[0][:rows])
-        b = f(inputs[1])
-        sec, n = timed(lambda: oracle.matmul(a, b), max_iters=3)
-        flops = 2.0 * rows * 8192 * 8192
-        return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": _blas_threads(),
-                "kind": "port",
-                "sample": f"{rows} of 8192 rows of the 8192^3 GEMM in float64 numpy, median of {n}"}
-    return None
+    use_all_cores()
+    t0 = time.perf_counter()
+    b.reference(*inputs)                     # warmup, and the size of one call
+    once = time.perf_counter() - t0
+    iters = max(1, min(20, int(15.0 / max(once, 1e-6))))
+    t = time_cpu(b.reference, *inputs, warmup=0, iters=iters)
+    value, unit, _ = _value_unit(name, meta, t["median_ms"])
+    return {"value": value, "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"full workload through the registry's torch-CPU Model spec "
+                      f"(torch {torch.__version__}, {torch.get_num_threads()} threads on "
+                      f"{H.cpu_model()}, {platform.machine()}); median of {iters} after 1 "
+                      f"warmup, {t['median_ms']:.1f} ms per step"}
 
 
 def _copy_calibration(n_bytes: int = 256 << 20, launches: int = 3) -> None:
@@ -373,7 +324,7 @@ def _run_workload(name, steps, warmup, want_cpu):
     del copies_in, copies_out
     torch.cuda.synchronize()
     if want_cpu:
-        rec["cpu_baseline"] = _cpu_baseline(name, inputs, meta)
+        rec["cpu_baseline"] = _cpu_baseline(name, b, inputs, meta)
     return rec
 
 

@@ -94,6 +94,12 @@ typedef struct mb_timing {
 #define MB_RUN_PARTS      2u  /* also time each kernel of a multi-kernel entry                 */
 #define MB_RUN_WALL_ONLY  4u  /* no events: iters launches back to back, one host sync; every
                                  statistic = host wall clock / iters (throughput timing)       */
+#define MB_RUN_COLD       8u  /* before each timed dispatch, outside its event pair, write a
+                                 library-owned 512 MiB buffer so no cache level (L2, the
+                                 256 MB memory-side cache) holds the kernel's inputs: the
+                                 harness's --cold-start (reference mlx/scripts/harness.py:403,
+                                 metal/scripts/timing.mm:236-246 purgeMetalCaches).  Not
+                                 with MB_RUN_WALL_ONLY.                                        */
 
 /* Device description; replaces detect_chip()/MChip (reference
  * metal/scripts/setup.h:26-46, setup.cpp:116-136). */

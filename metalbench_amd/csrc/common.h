@@ -43,6 +43,12 @@ uint32_t device_cu_count();               // compute units of the initialised de
 // Returns nullptr (and sets the error) on failure.
 void* library_workspace(size_t bytes, size_t zero_prefix, hipStream_t s);
 
+// Library-owned buffer twice the size of the memory-side cache, allocated on
+// first use and freed by mb_shutdown(); writing it evicts every cache level.
+void* library_flush_buffer(size_t* bytes);
+// Enqueue that eviction on `s` (copy.hip).
+int launch_cache_eviction(hipStream_t s);
+
 // ---- per-kernel timing marks ---------------------------------------------------
 // A multi-kernel entry calls mark(i, name) right before enqueuing kernel i.
 // When timing parts, mb_run records an event there.

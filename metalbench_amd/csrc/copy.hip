@@ -57,6 +57,16 @@ int launch_copy(const float* src, float* dst, uint64_t n, hipStream_t s) {
     return MB_OK;
 }
 
+// Cache eviction for cold timing (mb_run's MB_RUN_COLD): every lane writes
+// 16-byte vectors over the whole flush buffer, so what the timed kernel reads
+// next is no longer in the L2s or the 256 MB memory-side cache.
+__global__ __launch_bounds__(THREADS)
+void evict_kernel(uint4* __restrict__ buf, uint64_t n16, uint32_t stamp) {
+    const uint64_t stride = (uint64_t)gridDim.x * THREADS;
+    for (uint64_t i = (uint64_t)blockIdx.x * THREADS + threadIdx.x; i < n16; i += stride)
+        buf[i] = uint4{stamp, (uint32_t)i, (uint32_t)(i >> 32), stamp};
+}
+
 // Registry launcher: src@0 (input f32), dst@1 (output f32), n@2 (elements).
 int run_copy(const Bindings& bs, hipStream_t s, PartMarks*) {
     uint32_t n;
@@ -70,6 +80,17 @@ int run_copy(const Bindings& bs, hipStream_t s, PartMarks*) {
 }
 
 }  // namespace
+
+int launch_cache_eviction(hipStream_t s) {
+    static uint32_t stamp = 0;
+    size_t bytes = 0;
+    void* buf = library_flush_buffer(&bytes);
+    if (!buf) return MB_E_HIP;
+    hipLaunchKernelGGL(evict_kernel, dim3(device_cu_count() ? 4 * device_cu_count() : 1024), dim3(THREADS), 0, s,
+                       static_cast<uint4*>(buf), (uint64_t)(bytes / 16), ++stamp);
+    MB_LAUNCH_CHECK("cache eviction");
+    return MB_OK;
+}
 
 void register_copy() {
     register_kernel({"copy_f32", run_copy, reinterpret_cast<const void*>(&copy_f32_kernel), 1});

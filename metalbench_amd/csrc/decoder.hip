@@ -278,11 +278,15 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
         __builtin_amdgcn_sched_barrier(0);
     }
     // QKV: the RoPE rotation of pair (2i, 2i+1), i = tid % 64, at position
-    // cache_len, computed while the first loads are in flight
+    // cache_len, computed while the first loads are in flight.  The angle
+    // pos * base^(-2i/Dh) is formed and reduced mod 2 pi in fp64: an fp32
+    // angle would be off by ~pos * 6e-8 rad (0.06 rad at pos 10^6).
     float rope_cs = 1.f, rope_sn = 0.f;
     if (EPI == EPI_QKV) {
-        const float omega = powf(p.rope_base, -2.0f * (float)(tid & 63) / (float)DH);
-        sincosf((float)p.cache_len * omega, &rope_sn, &rope_cs);
+        const double omega = pow((double)p.rope_base, -2.0 * (double)(tid & 63) / (double)DH);
+        const double ang = (double)p.cache_len * omega;
+        constexpr double TWO_PI = 6.283185307179586476925;
+        sincosf((float)(ang - TWO_PI * rint(ang / TWO_PI)), &rope_sn, &rope_cs);
     }
 
     f32x4 acc[8];
@@ -860,10 +864,18 @@ struct Plan {
 // that.
 constexpr uint32_t KG = 32;   // K split granularity (rows)
 
+// The plan is a function of the shapes alone: it is sized for the 256 CUs of
+// a whole gfx950 device (MI350X / MI355X), not for the device in use, so
+// mb_decoder_step_workspace_bytes() gives the same answer before and after
+// mb_init() and on a partitioned device (which then runs several workgroups
+// per CU), and the split-K summation order -- hence every output bit -- does
+// not depend on the device.
+constexpr uint32_t PLAN_CUS = 256;
+
 static void choose_split(uint32_t tiles, uint32_t k, uint32_t ww, uint32_t* splits, uint32_t* kc,
                          uint32_t* ring) {
     const uint32_t groups = k / KG;
-    const uint32_t slots = std::max(device_cu_count(), 1u);
+    const uint32_t slots = PLAN_CUS;
     const uint32_t want = std::min(std::max(1u, slots / tiles), groups);
     const uint32_t per = cdiv(groups, want);
     *splits = cdiv(groups, per);
@@ -903,7 +915,7 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
         // faster than several per CU); splits of a multiple of 128 keys (an even
         // number of 64-key iterations, as the loop is unrolled by two)
         const uint32_t pairs = B * a->n_kv_heads;
-        const uint32_t want = std::max(1u, cdiv(std::max(device_cu_count(), 1u), pairs));
+        const uint32_t want = std::max(1u, cdiv(PLAN_CUS, pairs));
         const uint32_t nmax = std::max(1u, cdiv(a->cache_len, 2 * AKEYS));
         const uint32_t per = cdiv(std::max(a->cache_len, 1u), std::min(want, nmax));
         pl->split_keys = cdiv(per, 2 * AKEYS) * 2 * AKEYS;

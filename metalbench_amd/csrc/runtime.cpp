@@ -41,6 +41,7 @@ struct State {
     void* ws = nullptr;
     size_t ws_bytes = 0;
     size_t ws_zeroed = 0;   // bytes at the front of ws known to be zero
+    void* flush = nullptr;  // cache-eviction buffer (MB_RUN_COLD)
     uint32_t cu_count = 0;
 };
 static State g;
@@ -87,6 +88,24 @@ void* library_workspace(size_t bytes, size_t zero_prefix, hipStream_t s) {
     // This caller writes non-counter data right after its own counters.
     g.ws_zeroed = zero_prefix;
     return g.ws;
+}
+
+// 512 MiB: twice the 256 MB memory-side cache of an MI355X, far above the
+// 4 MB L2 of each XCD.
+constexpr size_t FLUSH_BYTES = (size_t)512 << 20;
+
+void* library_flush_buffer(size_t* bytes) {
+    if (!g.flush) {
+        hipError_t e = hipMalloc(&g.flush, FLUSH_BYTES);
+        if (e != hipSuccess) {
+            g.flush = nullptr;
+            fail(MB_E_HIP, "cache-eviction buffer hipMalloc(%zu) failed: %s", FLUSH_BYTES,
+                 hipGetErrorString(e));
+            return nullptr;
+        }
+    }
+    *bytes = FLUSH_BYTES;
+    return g.flush;
 }
 
 // ---- kernel registry ------------------------------------------------------------
@@ -225,6 +244,7 @@ int mb_shutdown(void) {
     if (!g.inited) return MB_OK;
     (void)hipDeviceSynchronize();
     if (g.ws) (void)hipFree(g.ws);
+    if (g.flush) (void)hipFree(g.flush);
     if (g.lib_stream) (void)hipStreamDestroy(g.lib_stream);
     g = State{};
     return MB_OK;
@@ -312,6 +332,9 @@ int mb_run(int id, const mb_binding* bindings, int n_bindings, int warmup, int i
         return fail(MB_E_ARG, "bad bindings array");
     if (warmup < 0) warmup = 0;
     if (iters <= 0) iters = 1;   // reference timing.mm:135
+    const bool cold = flags & MB_RUN_COLD;
+    if (cold && (flags & MB_RUN_WALL_ONLY))
+        return fail(MB_E_ARG, "MB_RUN_COLD needs event timing: not with MB_RUN_WALL_ONLY");
 
     Bindings bs;
     for (int i = 0; i < n_bindings; ++i) {
@@ -379,6 +402,10 @@ int mb_run(int id, const mb_binding* bindings, int n_bindings, int warmup, int i
     auto wall0 = std::chrono::steady_clock::now();
     for (int it = 0; it < iters; ++it) {
         hipEvent_t* e = pipelined ? &ev[(size_t)it * per_iter] : ev.data();
+        if (cold) {   // evict the caches, outside the event pair
+            int rc = launch_cache_eviction(s);
+            if (rc) { destroy(); return rc; }
+        }
         hipError_t r = hipEventRecord(e[0], s);
         if (r != hipSuccess) { destroy(); return fail(MB_E_HIP, "hipEventRecord: %s", hipGetErrorString(r)); }
         PartMarks pm;

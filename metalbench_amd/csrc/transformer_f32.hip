@@ -143,8 +143,12 @@ void matvec_kernel(const float* __restrict__ A, const float* __restrict__ x, flo
 
 // ---- prefill GQA attention -------------------------------------------------------------------
 
+// T is the arithmetic of the attention logits: q, k, the rotation, q.k and
+// the online softmax (float, or double for the decoder layer, see
+// run_llama_decoder_layer); v and the output stay fp32.
+template <typename T>
 struct AttnPrefillArgs {
-    const float* qkv;   // [S][ldq]: q at column h*Dh, k at D + kvh*Dh, v at D + Hkv*Dh + kvh*Dh
+    const T* qkv;       // [S][ldq]: q at column h*Dh, k at D + kvh*Dh, v at D + Hkv*Dh + kvh*Dh
     float* out;         // [S][ldo]: head h at column h*Dh
     uint32_t S, D, H, Hkv, ldq, ldo;
     float base, scale;  // RoPE base; 1 / sqrt(Dh)
@@ -152,94 +156,180 @@ struct AttnPrefillArgs {
 
 constexpr int QB = 64;   // queries per workgroup (and keys per LDS chunk)
 
+template <typename T> __device__ __forceinline__ T exp_t(T v);
+template <> __device__ __forceinline__ float exp_t<float>(float v) { return expf(v); }
+template <> __device__ __forceinline__ double exp_t<double>(double v) { return exp(v); }
+
+// Rotation of pair (2j, 2j+1) at position pos: angle pos * base^(-2j/Dh),
+// in fp64 (an fp32 angle is off by ~pos * 6e-8 rad).
+__device__ __forceinline__ void rope_cs(uint32_t pos, uint32_t pair, uint32_t dh, float base,
+                                        double* cs, double* sn) {
+    const double ang = (double)pos * pow((double)base, -2.0 * (double)pair / (double)dh);
+    *sn = sin(ang);
+    *cs = cos(ang);
+}
+
 // Workgroup (head h, 64 queries); lanes 4q .. 4q+3 own query q, DP = Dh/4
 // head dims each.  q and k are rotated by their positions (the row index)
 // with omega_j = base^(-2j/Dh) on interleaved pairs (2j, 2j+1).
-template <int DP>
+template <int DP, typename T>
 __global__ __launch_bounds__(256)
-void attention_prefill_kernel(AttnPrefillArgs a) {
+void attention_prefill_kernel(AttnPrefillArgs<T> a) {
     constexpr int DH = 4 * DP;
-    __shared__ __attribute__((aligned(16))) float ks[QB][DH];
+    __shared__ __attribute__((aligned(16))) T ks[QB][DH];
     __shared__ __attribute__((aligned(16))) float vs[QB][DH];
     const uint32_t tid = threadIdx.x;
     const uint32_t h = blockIdx.x, kvh = h / (a.H / a.Hkv);
     const uint32_t qi = blockIdx.y * QB + tid / 4, part = tid % 4, d0 = part * DP;
     const uint32_t kcol = a.D + kvh * DH, vcol = a.D + a.Hkv * DH + kvh * DH;
 
-    float q[DP];
+    T q[DP];
 #pragma unroll
     for (int j = 0; j < DP / 2; ++j) {
-        float x0 = 0.f, x1 = 0.f;
+        T x0 = 0, x1 = 0;
         if (qi < a.S) {
-            const float2 v = *reinterpret_cast<const float2*>(
-                a.qkv + (size_t)qi * a.ldq + h * DH + d0 + 2 * j);
-            x0 = v.x; x1 = v.y;
+            const T* src = a.qkv + (size_t)qi * a.ldq + h * DH + d0 + 2 * j;
+            x0 = src[0]; x1 = src[1];
         }
-        const uint32_t pair = d0 / 2 + j;
-        const float omega = powf(a.base, -2.0f * (float)pair / (float)DH);
-        float sn, cs;
-        sincosf((float)qi * omega, &sn, &cs);
-        q[2 * j] = x0 * cs - x1 * sn;
-        q[2 * j + 1] = x0 * sn + x1 * cs;
+        double cs, sn;
+        rope_cs(qi, d0 / 2 + j, DH, a.base, &cs, &sn);
+        q[2 * j] = x0 * (T)cs - x1 * (T)sn;
+        q[2 * j + 1] = x0 * (T)sn + x1 * (T)cs;
     }
 
-    float m_run = NEG_BIG, l_run = 0.f, o[DP];
+    T m_run = (T)NEG_BIG, l_run = 0;
+    T o[DP];
 #pragma unroll
-    for (int d = 0; d < DP; ++d) o[d] = 0.f;
+    for (int d = 0; d < DP; ++d) o[d] = 0;
 
     for (uint32_t kc = 0; kc < a.S; kc += QB) {
         __syncthreads();   // the previous chunk is no longer read
         for (uint32_t e = tid; e < QB * DH / 2; e += 256) {
             const uint32_t key = e / (DH / 2), pair = e % (DH / 2), kk = kc + key;
-            float2 kv = make_float2(0.f, 0.f), vv = make_float2(0.f, 0.f);
+            T k0 = 0, k1 = 0, v0 = 0, v1 = 0;
             if (kk < a.S) {
-                kv = *reinterpret_cast<const float2*>(a.qkv + (size_t)kk * a.ldq + kcol + 2 * pair);
-                vv = *reinterpret_cast<const float2*>(a.qkv + (size_t)kk * a.ldq + vcol + 2 * pair);
+                const T* kr = a.qkv + (size_t)kk * a.ldq + kcol + 2 * pair;
+                const T* vr = a.qkv + (size_t)kk * a.ldq + vcol + 2 * pair;
+                k0 = kr[0]; k1 = kr[1]; v0 = vr[0]; v1 = vr[1];
             }
-            const float omega = powf(a.base, -2.0f * (float)pair / (float)DH);
-            float sn, cs;
-            sincosf((float)kk * omega, &sn, &cs);
-            ks[key][2 * pair] = kv.x * cs - kv.y * sn;
-            ks[key][2 * pair + 1] = kv.x * sn + kv.y * cs;
-            vs[key][2 * pair] = vv.x;
-            vs[key][2 * pair + 1] = vv.y;
+            double cs, sn;
+            rope_cs(kk, pair, DH, a.base, &cs, &sn);
+            ks[key][2 * pair] = k0 * (T)cs - k1 * (T)sn;
+            ks[key][2 * pair + 1] = k0 * (T)sn + k1 * (T)cs;
+            vs[key][2 * pair] = (float)v0;
+            vs[key][2 * pair + 1] = (float)v1;
         }
         __syncthreads();
         const uint32_t nk = min((uint32_t)QB, a.S - kc);
         for (uint32_t j = 0; j < nk; ++j) {
-            float dot = 0.f;
+            T dot = 0;
 #pragma unroll
             for (int d = 0; d < DP; ++d) dot += q[d] * ks[j][d0 + d];
             dot += __shfl_xor(dot, 1);
             dot += __shfl_xor(dot, 2);
-            const float sc = dot * a.scale;
-            const float m_new = fmaxf(m_run, sc);
-            const float alpha = expf(m_run - m_new), p = expf(sc - m_new);
+            const T sc = dot * (T)a.scale;
+            const T m_new = m_run > sc ? m_run : sc;
+            const T alpha = exp_t<T>(m_run - m_new), p = exp_t<T>(sc - m_new);
             l_run = l_run * alpha + p;
 #pragma unroll
-            for (int d = 0; d < DP; ++d) o[d] = o[d] * alpha + p * vs[j][d0 + d];
+            for (int d = 0; d < DP; ++d) o[d] = o[d] * alpha + p * (T)vs[j][d0 + d];
             m_run = m_new;
         }
     }
     if (qi < a.S) {
-        const float inv = 1.0f / l_run;
+        const T inv = (T)1 / l_run;
 #pragma unroll
         for (int d = 0; d < DP; d += 2)
             *reinterpret_cast<float2*>(a.out + (size_t)qi * a.ldo + h * DH + d0 + d) =
-                make_float2(o[d] * inv, o[d + 1] * inv);
+                make_float2((float)(o[d] * inv), (float)(o[d + 1] * inv));
     }
 }
 
-int launch_attention_prefill(const AttnPrefillArgs& a, uint32_t dh, hipStream_t s) {
+template <typename T>
+int launch_attention_prefill(const AttnPrefillArgs<T>& a, uint32_t dh, hipStream_t s) {
     if (a.S == 0) return MB_OK;
     const dim3 grid(a.H, cdiv(a.S, QB)), block(256);
     switch (dh) {
-        case 32: hipLaunchKernelGGL(attention_prefill_kernel<8>, grid, block, 0, s, a); break;
-        case 64: hipLaunchKernelGGL(attention_prefill_kernel<16>, grid, block, 0, s, a); break;
-        case 128: hipLaunchKernelGGL(attention_prefill_kernel<32>, grid, block, 0, s, a); break;
+        case 32: hipLaunchKernelGGL((attention_prefill_kernel<8, T>), grid, block, 0, s, a); break;
+        case 64: hipLaunchKernelGGL((attention_prefill_kernel<16, T>), grid, block, 0, s, a); break;
+        case 128: hipLaunchKernelGGL((attention_prefill_kernel<32, T>), grid, block, 0, s, a); break;
         default: return fail(MB_E_ARG, "attention: head dim %u not 32, 64 or 128", dh);
     }
     MB_LAUNCH_CHECK("attention prefill");
+    return MB_OK;
+}
+
+// ---- fp64 RMSNorm GEMM (the decoder layer's q|k|v projection) -----------------------------
+
+// C[S][N] = rmsnorm(A) B in fp64 from fp32 A [S][K] and B [K][N]: each
+// workgroup computes a 64 x 64 tile, thread (ty, tx) the 4 x 4 outputs of rows
+// 4 ty .. 4 ty + 3 and columns tx, tx + 16, tx + 32, tx + 48; A and B go
+// through LDS 32 k at a time, widened to fp64 on the way in.  The row scale
+// rsqrt(mean(a^2) + eps) is accumulated from the same A chunks.
+constexpr int G64 = 64, GK = 32;
+
+__global__ __launch_bounds__(256)
+void rms_gemm_f64_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                         double* __restrict__ C, uint32_t S, uint32_t N, uint32_t K, float eps) {
+    __shared__ double as[G64][GK + 1];
+    __shared__ double bs[GK][G64 + 1];
+    __shared__ double rs[G64];
+    const uint32_t tid = threadIdx.x, tx = tid % 16, ty = tid / 16;
+    const uint32_t row0 = blockIdx.y * G64, col0 = blockIdx.x * G64;
+    double acc[4][4] = {};
+    double ss = 0;   // sum of squares of row row0 + tid / 4, quarter tid % 4 of each chunk
+    for (uint32_t k0 = 0; k0 < K; k0 += GK) {
+        __syncthreads();
+        for (uint32_t e = tid; e < G64 * GK; e += 256) {
+            const uint32_t r = e / GK, c = e % GK;
+            const uint32_t gr = row0 + r, gk = k0 + c;
+            as[r][c] = (gr < S && gk < K) ? (double)A[(size_t)gr * K + gk] : 0.0;
+            const uint32_t kr = e / G64, nc = e % G64;
+            bs[kr][nc] = (k0 + kr < K && col0 + nc < N) ? (double)B[(size_t)(k0 + kr) * N + col0 + nc]
+                                                        : 0.0;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < GK / 4; ++c) {
+            const double v = as[tid / 4][(tid % 4) * (GK / 4) + c];
+            ss += v * v;
+        }
+#pragma unroll 4
+        for (int kk = 0; kk < GK; ++kk) {
+            double av[4], bv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) av[i] = as[4 * ty + i][kk];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bv[j] = bs[kk][tx + 16 * j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] += av[i] * bv[j];
+        }
+    }
+    ss += __shfl_xor(ss, 1);
+    ss += __shfl_xor(ss, 2);
+    if (tid % 4 == 0) rs[tid / 4] = 1.0 / sqrt(ss / (double)K + (double)eps);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t r = row0 + 4 * ty + i;
+        if (r >= S) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t c = col0 + tx + 16 * j;
+            if (c < N) C[(size_t)r * N + c] = acc[i][j] * rs[4 * ty + i];
+        }
+    }
+}
+
+int launch_rms_gemm_f64(const float* a, const float* b, double* c, uint32_t S, uint32_t N,
+                        uint32_t K, float eps, hipStream_t s) {
+    if (S == 0 || N == 0) return MB_OK;
+    if (K == 0) return fail(MB_E_ARG, "rms gemm: K must be positive");
+    hipLaunchKernelGGL(rms_gemm_f64_kernel, dim3(cdiv(N, G64), cdiv(S, G64)), dim3(256), 0, s,
+                       a, b, c, S, N, K, eps);
+    MB_LAUNCH_CHECK("rms_gemm_f64");
     return MB_OK;
 }
 
@@ -360,7 +450,7 @@ int run_llama_attention(const Bindings& bs, hipStream_t s, PartMarks*) {
     if ((rc = launch_gemm_f32_ex(gemm_f32_args((const float*)x, (const float*)wqkv, qkv, S, nqkv, D),
                                  GEMM_F32_PLAIN, 1, s)))
         return rc;
-    AttnPrefillArgs a{qkv, attn, S, D, H, HKV, nqkv, D, base, 1.0f / sqrtf((float)dh)};
+    AttnPrefillArgs<float> a{qkv, attn, S, D, H, HKV, nqkv, D, base, 1.0f / sqrtf((float)dh)};
     if ((rc = launch_attention_prefill(a, dh, s))) return rc;
     return launch_gemm_f32_ex(gemm_f32_args(attn, (const float*)wo, (float*)y, S, D, D),
                               GEMM_F32_PLAIN, 1, s);
@@ -369,8 +459,15 @@ int run_llama_attention(const Bindings& bs, hipStream_t s, PartMarks*) {
 // llama_decoder_layer (prefill): x@0 [S][D], W_qkv@1, W_o@2, W_gu@3 [D][2 FF]
 // ([gate | up]), W_down@4 [FF][D], y@5 [S][D], S@6, D@7, H@8, H_kv@9, FF@10,
 // base@11, eps@12.  Five launches:
-//   qkv  = rmsnorm(x) W_qkv                    (RMS row scale in the GEMM)
-//   attn = attention(RoPE(q), RoPE(k), v)
+//   qkv  = rmsnorm(x) W_qkv                    (fp64, RMS row scale in the GEMM)
+//   attn = attention(RoPE(q), RoPE(k), v)      (fp64 logits and softmax)
+// The attention logits are the ill-conditioned part of this entry: with the
+// reference's normal(0, 1) weights q.k / sqrt(Dh) reaches the hundreds, so
+// fp32 rounding of q, k and the dot products moves the softmax weights of
+// near-tied keys, and the FFN amplifies it; an all-fp32 evaluation of the
+// layer lands ~0.15 from float64 on outputs of up to ~6000, one with fp64 q|k|v
+// and logits ~0.004.  At S = 64, D = 128 the fp64 work is a few hundred
+// thousand multiply-adds.
 //   x1   = x + attn W_o                        (residual in the epilogue)
 //   act  = silu(rmsnorm(x1) W_gate) * (rmsnorm(x1) W_up)
 //   y    = x1 + act W_down
@@ -394,26 +491,25 @@ int run_llama_decoder_layer(const Bindings& bs, hipStream_t s, PartMarks* pm) {
         (rc = bs.buffer(5, MB_DTYPE_F32, (uint64_t)S * D * 4, true, &y, "y")))
         return rc;
     auto al = [](size_t v) { return (v + 255) & ~(size_t)255; };
-    const size_t o_qkv = 0, o_attn = al((size_t)S * nqkv * 4),
+    const size_t o_qkv = 0, o_attn = al((size_t)S * nqkv * 8),
                  o_x1 = o_attn + al((size_t)S * D * 4), o_act = o_x1 + al((size_t)S * D * 4),
                  total = o_act + al((size_t)S * FF * 4);
     uint8_t* ws = static_cast<uint8_t*>(library_workspace(total, 0, s));
     if (!ws) return MB_E_HIP;
-    float* qkv = reinterpret_cast<float*>(ws + o_qkv);
+    double* qkv = reinterpret_cast<double*>(ws + o_qkv);
     float* attn = reinterpret_cast<float*>(ws + o_attn);
     float* x1 = reinterpret_cast<float*>(ws + o_x1);
     float* act = reinterpret_cast<float*>(ws + o_act);
     auto mark = [&](const char* n) { if (pm) pm->mark(s, n); };
 
     mark("qkv_rmsnorm");
-    GemmF32Args g = gemm_f32_args((const float*)x, (const float*)wqkv, qkv, S, nqkv, D);
-    g.eps = eps;
-    if ((rc = launch_gemm_f32_ex(g, GEMM_F32_RMS, 1, s))) return rc;
+    if ((rc = launch_rms_gemm_f64((const float*)x, (const float*)wqkv, qkv, S, nqkv, D, eps, s)))
+        return rc;
     mark("attention");
-    AttnPrefillArgs a{qkv, attn, S, D, H, HKV, nqkv, D, base, 1.0f / sqrtf((float)dh)};
+    AttnPrefillArgs<double> a{qkv, attn, S, D, H, HKV, nqkv, D, base, 1.0f / sqrtf((float)dh)};
     if ((rc = launch_attention_prefill(a, dh, s))) return rc;
     mark("wo_residual");
-    g = gemm_f32_args(attn, (const float*)wo, x1, S, D, D);
+    GemmF32Args g = gemm_f32_args(attn, (const float*)wo, x1, S, D, D);
     g.r = (const float*)x;
     if ((rc = launch_gemm_f32_ex(g, GEMM_F32_RESID, 1, s))) return rc;
     mark("gate_up_swiglu");
@@ -440,9 +536,9 @@ void register_transformer_f32() {
     register_kernel({"matvec_f32", run_matvec,
                      reinterpret_cast<const void*>(&matvec_kernel<true>), 1});
     register_kernel({"llama_attention_f32", run_llama_attention,
-                     reinterpret_cast<const void*>(&attention_prefill_kernel<8>), 1});
+                     reinterpret_cast<const void*>(&attention_prefill_kernel<8, float>), 1});
     register_kernel({"llama_decoder_layer_f32", run_llama_decoder_layer,
-                     reinterpret_cast<const void*>(&attention_prefill_kernel<8>), 5});
+                     reinterpret_cast<const void*>(&attention_prefill_kernel<8, double>), 5});
 }
 
 }  // namespace mb

@@ -2,7 +2,7 @@
 
     python mlx/scripts/harness.py <name> [--target speed|compute|memory|stable|balanced]
                                          [--iters 200] [--warmup 10] [--seed 0]
-                                         [--save] [--no-session] [--dry-run]
+                                         [--save] [--no-session] [--dry-run] [--cold-start]
                                          [--mlx-only | --metal-only] [--cpu-iters N]
 
 Same flow, report text, exit codes and persistence as reference
@@ -99,15 +99,18 @@ def _cpu_iters(b, iters, override):
 
 
 def evaluate(name, *, seed, warmup, iters, dry_run=False, profile=False, solo=None,
-             cpu_iters=None):
+             cpu_iters=None, cold_start=False):
     b = H.load_baseline(name)
     inputs = b.make_inputs(seed)
-    chip = H.chip_info()
+    # --mlx-only and --dry-run make no GPU call
+    chip = H.host_chip_info() if (solo == "mlx" or dry_run) else H.chip_info()
     c_iters = _cpu_iters(b, iters, cpu_iters)
 
     if solo == "mlx":
         ref_out = b.reference(*inputs)
-        r_t = time_cpu(b.reference, *inputs, warmup=1, iters=c_iters)
+        r_t = time_cpu(b.reference, *inputs, warmup=0 if cold_start else 1, iters=c_iters)
+        if cold_start:
+            r_t["cold_start"] = True
         return {"task": name, "chip": chip, "solo": "mlx",
                 "reference_timing": r_t, "correct": True,
                 "metrics": {"stability": max(0.0,
@@ -120,7 +123,15 @@ def evaluate(name, *, seed, warmup, iters, dry_run=False, profile=False, solo=No
     if dry_run:
         return {"task": name, "dry_run": True, "manifest": manifest}
 
-    k_t, kernel_outs = _run_native(b, inputs, warmup, iters)
+    # --cold-start: no warmup, and every timed dispatch starts with the caches
+    # evicted (the reference clears MLX's caches and drops the warmup, its
+    # timing.py:46-48; its host can purge its buffers, timing.mm:236-246)
+    if cold_start:
+        warmup = 0
+    k_t, kernel_outs = _run_native(b, inputs, warmup, iters,
+                                   native.RUN_COLD if cold_start else native.RUN_SYNC_EACH)
+    if cold_start:
+        k_t["cold_start"] = True
 
     def _kernel_metrics(m):
         median_s = k_t["median_ms"] / 1000.0
@@ -143,8 +154,11 @@ def evaluate(name, *, seed, warmup, iters, dry_run=False, profile=False, solo=No
 
     ref_out = b.reference(*inputs)
     ref_outs = list(ref_out) if isinstance(ref_out, (list, tuple)) else [ref_out]
-    r_t = time_cpu(b.reference, *inputs, warmup=1 if c_iters > 1 else 0, iters=c_iters)
+    r_t = time_cpu(b.reference, *inputs, warmup=1 if c_iters > 1 and not cold_start else 0,
+                   iters=c_iters)
     r_t["label"] = "cpu spec (torch, %d threads)" % r_t.get("threads", 0)
+    if cold_start:
+        r_t["cold_start"] = True
 
     if len(kernel_outs) != len(ref_outs):
         raise RuntimeError(f"{name}: kernel={len(kernel_outs)} outputs, ref={len(ref_outs)}")
@@ -418,6 +432,8 @@ def main(argv=None):
     ap.add_argument("--cpu-iters", type=int, default=None,
                     help="iterations of the CPU spec timing (default: registry cpu_iters)")
     ap.add_argument("--dry-run", action="store_true")
+    ap.add_argument("--cold-start", action="store_true",
+                    help="no warmup; evict every cache level before each timed dispatch")
     ap.add_argument("--profile", action="store_true",
                     help="hardware counters of one extra dispatch, from rocprofv3 --pmc passes")
     ap.add_argument("--save", action="store_true",
@@ -438,8 +454,9 @@ def main(argv=None):
     if not args.name:
         ap.error("kernel name required (or use --all from bench script)")
 
-    chip = H.chip_info()
-    if solo_mode != "mlx" and not args.dry_run and chip["type"] != "gfx950":
+    gpu_call = solo_mode != "mlx" and not args.dry_run
+    chip = H.chip_info() if gpu_call else H.host_chip_info()
+    if gpu_call and chip["type"] != "gfx950":
         sys.exit(f"[error] this backend requires an AMD gfx950 (MI355X) GPU. "
                  f"Detected: {chip.get('error', chip['name'])!r}.")
 
@@ -459,7 +476,7 @@ def main(argv=None):
 
     result = evaluate(args.name, seed=args.seed, warmup=args.warmup, iters=args.iters,
                       dry_run=args.dry_run, profile=args.profile, solo=solo_mode,
-                      cpu_iters=args.cpu_iters)
+                      cpu_iters=args.cpu_iters, cold_start=args.cold_start)
 
     if args.dry_run:
         print(json.dumps(result["manifest"], indent=2))

@@ -348,6 +348,35 @@ def chip_info() -> dict:
                 "hbm_bytes": 0, "clock_khz": 0, "cpu_model": cpu_model(), "error": str(e)}
 
 
+def _kfd_gfx_targets() -> list[str]:
+    """gfx targets of the GPUs the kernel driver lists, read from the KFD
+    topology in sysfs (no HIP call, so no device is initialised): a node's
+    gfx_target_version 90500 is gfx950."""
+    out = []
+    try:
+        for props in sorted(Path("/sys/class/kfd/kfd/topology/nodes").glob("*/properties")):
+            for line in props.read_text().splitlines():
+                key, _, val = line.partition(" ")
+                if key == "gfx_target_version" and val.strip().isdigit() and int(val) > 0:
+                    v = int(val)
+                    out.append(f"gfx{v // 10000}{(v // 100) % 100:x}{v % 100:x}")
+    except Exception:
+        pass
+    return out
+
+
+def host_chip_info() -> dict:
+    """chip_info() without touching the GPU, for the modes that make no GPU call
+    (--mlx-only, --dry-run): the gfx target comes from the KFD topology, and
+    the marketing name is not queried."""
+    targets = _kfd_gfx_targets()
+    arch = targets[0] if targets else "unknown"
+    name = f"AMD {arch} (not queried)" if targets else "unknown"
+    return {"type": arch, "name": name, "bucket": bucket_key_from_name(name),
+            "cpu_cores": os.cpu_count() or 0, "gpu_cores": 0, "ram_bytes": _host_ram_bytes(),
+            "hbm_bytes": 0, "clock_khz": 0, "cpu_model": cpu_model()}
+
+
 def bucket_key_from_name(name):
     s = "".join((c.lower() if c.isalnum() else "-") for c in name)
     while "--" in s:

@@ -32,6 +32,7 @@ RUN_SYNC_EACH = 0
 RUN_PIPELINED = 1
 RUN_PARTS = 2
 RUN_WALL_ONLY = 4
+RUN_COLD = 8
 MAX_PARTS = 8
 
 

@@ -20,13 +20,28 @@ def cpu_threads() -> int:
         return os.cpu_count() or 1
 
 
+def use_all_cores() -> int:
+    """Give torch's CPU kernels every host core (its default is the physical
+    core count, which may be fewer); returns the thread count."""
+    try:
+        import torch
+        n = os.cpu_count() or 1
+        if torch.get_num_threads() != n:
+            torch.set_num_threads(n)
+        return torch.get_num_threads()
+    except Exception:
+        return os.cpu_count() or 1
+
+
 def warm(fn: Callable[..., Any], *args, n: int = 1) -> None:
     for _ in range(n):
         fn(*args)
 
 
 def time_cpu(fn: Callable[..., Any], *args, warmup: int = 1, iters: int = 5) -> dict:
-    """Time `fn(*args)` with time.perf_counter (reference timing.py:54-58)."""
+    """Time `fn(*args)` with time.perf_counter (reference timing.py:54-58), on
+    every host core."""
+    use_all_cores()
     if iters <= 0:
         iters = 1
     for _ in range(warmup):

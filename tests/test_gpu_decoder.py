@@ -159,3 +159,37 @@ def test_decoder_step_library_workspace_across_shape_changes(mb, dev):
         ins = _make(*cfg, seed=7)
         B, D, H, HKV, FF, L = cfg
         _check(_run(dev, ins, *cfg), _want(ins, H, HKV, L), f"sequence {cfg}")
+
+
+def test_decoder_workspace_size_does_not_depend_on_init(dev):
+    """mb_decoder_step_workspace_bytes() is callable before mb_init() and must
+    give the size a launch after mb_init() checks against."""
+    cfg = (16, 2048, 16, 4, 1536, 1000)
+    B, D, H, HKV, FF, L = cfg
+    a = native.MbDecoderStepArgs(batch=B, d_model=D, n_heads=H, n_kv_heads=HKV, head_dim=128,
+                                 d_ff=FF, cache_len=L, cache_stride=L, rope_base=500000.0,
+                                 eps=1e-5)
+    native.shutdown()
+    before = native.load().mb_decoder_step_workspace_bytes(ctypes.byref(a))
+    native.init(0)
+    after = native.load().mb_decoder_step_workspace_bytes(ctypes.byref(a))
+    assert before == after > 0
+    ins = _make(*cfg, seed=11)
+    ws = torch.zeros(before, dtype=torch.uint8, device=dev)
+    _check(_run(dev, ins, *cfg, workspace=ws), _want(ins, H, HKV, L), "pre-init workspace size")
+
+
+def test_decoder_step_rope_at_large_position(mb, dev):
+    """The new token at position 10^6: its RoPE angle pos * base^(-2i/Dh) must be
+    formed in fp64 (in fp32 the first pairs' angles are off by 0.03-0.08 rad,
+    i.e. several percent of k_new, far above bf16 rounding)."""
+    B, D, H, HKV, FF, L = 1, 256, 2, 1, 256, 1_000_000
+    ins = _make(B, D, H, HKV, FF, L, seed=13)
+    got = _run(dev, ins, B, D, H, HKV, FF, L)
+    want = _want(ins, H, HKV, L)
+    _check(got, want, "pos 1e6")
+    kn, wk = oracle.as_f64(got[1]), want[1]
+    pair = np.sqrt(wk[..., 0::2] ** 2 + wk[..., 1::2] ** 2).repeat(2, axis=-1)
+    bad = np.abs(kn - wk) > 2.0 ** -8 * np.abs(wk) + 1e-4 * pair
+    assert not bad.any(), f"k_new: {int(bad.sum())} of {kn.size} beyond bf16 rounding, " \
+                          f"max |diff| {np.abs(kn - wk).max():.3e}"

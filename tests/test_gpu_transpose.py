@@ -5,7 +5,8 @@ import pytest
 import torch
 
 import oracle
-from gpu_util import bits32, launch, ptr, run_registry, seeded
+from gpu_util import bits32, launch, ptr, run_bound, run_registry, seeded
+from metalbench_amd import native
 
 pytestmark = pytest.mark.gpu
 
@@ -61,3 +62,30 @@ def test_transpose_registry_config(mb, name):
     b, inputs, outs, _ = run_registry(name, seed=0)
     want = oracle.transpose(inputs[0].numpy())
     assert np.array_equal(outs[0].numpy().view(np.int32), want.view(np.int32))
+
+
+def test_cold_start_timing_evicts_and_keeps_results(mb):
+    """mb_run with MB_RUN_COLD (the harness's --cold-start): every timed
+    dispatch follows a cache eviction outside its event pair; the output is
+    still bit exact, and the flag is refused with MB_RUN_WALL_ONLY."""
+    import torch
+    from metalbench_amd import helpers as H
+    b = H.load_baseline("transpose_2d_ref")
+    a = b.make_inputs(0)[0]
+    (got,) = run_bound("transpose_2d_f32", [(0, a)], [(1, (2048, 1024))],
+                       [(2, "u32", 1024), (3, "u32", 2048)])
+    assert np.array_equal(bits32(got), bits32(a.t().contiguous()))
+    dev = torch.device("cuda", 0)
+    da, db = a.to(dev), torch.empty(2048, 1024, device=dev)
+    binds = [native.make_binding(0, native.ROLE_INPUT, "f32", da.data_ptr(), da.numel() * 4),
+             native.make_binding(1, native.ROLE_OUTPUT, "f32", db.data_ptr(), db.numel() * 4),
+             native.make_binding(2, native.ROLE_SCALAR, "u32", value=1024),
+             native.make_binding(3, native.ROLE_SCALAR, "u32", value=2048)]
+    kid = native.kernel_find("transpose_2d_f32")
+    t = native.run(kid, binds, 0, 3, native.RUN_COLD)
+    assert t["iters"] == 3 and 0 < t["min_ms"] <= t["median_ms"]
+    torch.cuda.synchronize()
+    assert np.array_equal(bits32(db), bits32(a.t().contiguous()))
+    with pytest.raises(native.NativeError) as e:
+        native.run(kid, binds, 0, 2, native.RUN_COLD | native.RUN_WALL_ONLY)
+    assert e.value.code == -7

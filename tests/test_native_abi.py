@@ -74,5 +74,9 @@ def test_decoder_workspace_size_without_gpu():
                                  rope_base=500000.0, eps=1e-5)
     n = native.load().mb_decoder_step_workspace_bytes(ctypes.byref(a))
     assert 0 < n < (1 << 30), native.last_error()
+    # The plan does not depend on mb_init(): without a device the size already
+    # holds the split-K partials of the whole-device grid, e.g. gate/up's 56
+    # tiles x 4 splits of 16 x 512 fp32 (a plan for one CU would need 1 split).
+    assert n >= 56 * 4 * 16 * 512 * 4
     a.head_dim = 64
     assert native.load().mb_decoder_step_workspace_bytes(ctypes.byref(a)) == 0

@@ -92,9 +92,13 @@ def test_matmul_models_match_oracle():
     for name in ("sqr_mm", "rect_mm"):
         got = _load_model(name).forward(a, c).numpy()
         assert np.allclose(got, oracle.matmul(a.numpy(), c.numpy()), rtol=1e-5, atol=1e-5)
+    # large_mm's spec is the bf16 product: the fp32-accumulated sum rounded to
+    # bf16 once, i.e. within half a bf16 ulp (2^-8 relative) of the exact product
     ab, cb = a.to(torch.bfloat16), c.to(torch.bfloat16)
-    got = _load_model("large_mm").forward(ab, cb).numpy()
-    assert np.allclose(got, oracle.matmul(oracle.as_f64(ab), oracle.as_f64(cb)), rtol=1e-5, atol=1e-5)
+    got = _load_model("large_mm").forward(ab, cb)
+    assert got.dtype == torch.bfloat16
+    exact = oracle.matmul(oracle.as_f64(ab), oracle.as_f64(cb))
+    assert np.all(np.abs(oracle.as_f64(got) - exact) <= 2.0 ** -8 * np.abs(exact) * 1.0001 + 1e-6)
 
 
 def test_transpose_model_matches_oracle():
