@@ -260,6 +260,20 @@ uint64_t mb_decoder_step_workspace_bytes(const mb_decoder_step_args* args);
  * uses (and grows) its own workspace. */
 int mb_launch_llama_decoder_step_bf16(const mb_decoder_step_args* args, void* stream);
 
+/* The same decode step, allocating nothing.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory during the call (code
+ * under HIP graph capture, allocation-free serving loops, harnesses that
+ * forbid hipMalloc).  The workspace is a static device array of
+ * MB_DECODER_NOALLOC_MAX_BYTES carried by the library's code object (one per
+ * device, held until the process ends), so `args->workspace` must be NULL;
+ * shapes whose mb_decoder_step_workspace_bytes() exceeds the limit are
+ * rejected with MB_E_ARG.  Results are bit-identical to
+ * mb_launch_llama_decoder_step_bf16.  Every call on a device shares that
+ * device's scratch and a call leaves its intermediates there: calls that
+ * overlap on one device (two streams, two threads) race. */
+#define MB_DECODER_NOALLOC_MAX_BYTES (32u << 20)
+int mb_launch_llama_decoder_step_bf16_noalloc(const mb_decoder_step_args* args, void* stream);
+
 /* Plain fp32 copy dst[i] = src[i]: the calibration kernel for HBM traffic
  * counters and the measured-bandwidth ceiling.  No reference counterpart. */
 int mb_launch_copy_f32(const float* src, float* dst, uint64_t n, void* stream);

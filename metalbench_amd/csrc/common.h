@@ -92,6 +92,9 @@ void register_gemm_f32();
 void register_conv2d();
 void register_gemm_bf16();
 void register_decoder();
+// Looks up the allocation-free decoder entry point's device scratch on the
+// current device (decoder.hip); mb_init() calls it once the device is set.
+int init_decoder_scratch();
 void register_transformer_f32();
 
 static inline uint32_t cdiv(uint32_t a, uint32_t b) { return (a + b - 1) / b; }

@@ -45,6 +45,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 
 namespace mb {
 namespace {
@@ -1124,7 +1125,92 @@ int run_decoder(const Bindings& bs, hipStream_t s, PartMarks* pm) {
     return launch_decoder(&a, s, pm);
 }
 
+// ---- allocation-free entry point ------------------------------------------------------
+// mb_launch_llama_decoder_step_bf16_noalloc runs the same five kernels with
+// their workspace in `scratch`, a file-scope device array that the code
+// object carries, so the call allocates nothing (callers under HIP graph
+// capture or in allocation-free serving loops).  Each device holds its own
+// copy of the array for the life of the process; host code uses the device
+// address hipGetSymbolAddress returns for it (kept per device in
+// g_scratch), never the array's name, which in host code is only a
+// host-side stand-in.  Only the completion counters at the front of the
+// workspace must start at zero, and the kernels leave them at zero; a call
+// whose counters reach past what is known to be zero (the first call on a
+// device, or a shape with more counters than any before) clears them first
+// with a fill kernel (a kernel, not hipMemsetAsync, so that graph capture
+// records a plain kernel node).  Every call on a device shares its scratch:
+// calls that overlap on one device race.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)32 << 20;   // 32 MiB (9.6 MB at the BASELINE shape)
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+static_assert(NOALLOC_SCRATCH_BYTES == MB_DECODER_NOALLOC_MAX_BYTES, "mbhip.h states the limit");
+
+constexpr int MAX_DEVICES = 64;
+struct DeviceScratch {
+    void* ptr = nullptr;     // device address of `scratch` on that device
+    size_t zeroed = 0;       // leading bytes known to be zero
+};
+DeviceScratch g_scratch[MAX_DEVICES];
+std::mutex g_scratch_mutex;
+
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* __restrict__ p, uint32_t n) {
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0u;
+}
+
+// Looks up the scratch of the current device (once per device, with that
+// device current).
+int scratch_of_current_device(DeviceScratch** out) {
+    int dev = -1;
+    MB_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= MAX_DEVICES)
+        return fail(MB_E_NO_DEVICE, "decoder scratch: device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    DeviceScratch& d = g_scratch[dev];
+    if (!d.ptr) {
+        void* ptr = nullptr;
+        hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(MB_E_HIP, "hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                        hipGetErrorString(e));
+        d.ptr = ptr;
+        d.zeroed = 0;
+    }
+    *out = &d;
+    return MB_OK;
+}
+
+int launch_decoder_noalloc(const mb_decoder_step_args* a, hipStream_t s) {
+    Plan pl;
+    int rc = make_plan(a, &pl);
+    if (rc) return rc;
+    if (a->workspace)
+        return fail(MB_E_ARG, "decoder step (no-alloc): workspace must be NULL, this entry point "
+                              "uses the library's static scratch");
+    if (pl.total > NOALLOC_SCRATCH_BYTES)
+        return fail(MB_E_ARG, "decoder step (no-alloc): these shapes need %zu bytes of scratch; "
+                              "the static scratch holds %zu", pl.total, NOALLOC_SCRATCH_BYTES);
+    DeviceScratch* d = nullptr;
+    if ((rc = scratch_of_current_device(&d))) return rc;
+    const size_t zero = counters_bytes(pl);
+    if (zero > d->zeroed) {
+        const uint32_t words = (uint32_t)(zero / 4);   // counters_bytes is 256-byte aligned
+        hipLaunchKernelGGL(zero_words_kernel, dim3(std::min(cdiv(words, 256u), 1024u)), dim3(256),
+                           0, s, static_cast<uint32_t*>(d->ptr), words);
+        MB_LAUNCH_CHECK("decoder scratch clear");
+    }
+    // this call's non-counter data starts right after its counters
+    d->zeroed = zero;
+    mb_decoder_step_args b = *a;
+    b.workspace = d->ptr;
+    b.workspace_bytes = NOALLOC_SCRATCH_BYTES;
+    return launch_decoder(&b, s, nullptr);
+}
+
 }  // namespace
+
+int init_decoder_scratch() {
+    DeviceScratch* d = nullptr;
+    return scratch_of_current_device(&d);
+}
 
 void register_decoder() {
     register_kernel({"llama_decoder_step_bf16", run_decoder,
@@ -1144,4 +1230,11 @@ extern "C" int mb_launch_llama_decoder_step_bf16(const mb_decoder_step_args* arg
     mb::clear_error();
     if (!mb::initialized()) return mb::fail(MB_E_STATE, "mb_init() has not been called");
     return mb::launch_decoder(args, mb::stream_or_default(stream), nullptr);
+}
+
+extern "C" int mb_launch_llama_decoder_step_bf16_noalloc(const mb_decoder_step_args* args,
+                                                         void* stream) {
+    mb::clear_error();
+    if (!mb::initialized()) return mb::fail(MB_E_STATE, "mb_init() has not been called");
+    return mb::launch_decoder_noalloc(args, mb::stream_or_default(stream));
 }

@@ -236,6 +236,10 @@ int mb_init(int ordinal) {
     g.cu_count = (uint32_t)p.multiProcessorCount;
     g.inited = true;
     (void)registry();
+    // The allocation-free decoder entry point's scratch address on this
+    // device; if the lookup fails here, that entry point retries it on its
+    // first call and reports the error there.
+    if (init_decoder_scratch() != MB_OK) clear_error();
     return MB_OK;
 }
 

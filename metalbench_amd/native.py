@@ -114,6 +114,7 @@ SIGNATURES = {
                                   + [c_void_p]),
     "mb_decoder_step_workspace_bytes": (c_uint64, [POINTER(MbDecoderStepArgs)]),
     "mb_launch_llama_decoder_step_bf16": (c_int, [POINTER(MbDecoderStepArgs), c_void_p]),
+    "mb_launch_llama_decoder_step_bf16_noalloc": (c_int, [POINTER(MbDecoderStepArgs), c_void_p]),
     "mb_launch_copy_f32": (c_int, [c_void_p, c_void_p, c_uint64, c_void_p]),
 }
 
