@@ -36,9 +36,18 @@ $(OBJ_DIR)/%.hip.o: $(SRC_DIR)/%.hip $(HEADERS)
 	@mkdir -p $(OBJ_DIR)
 	$(HIPCC) $(HIPFLAGS) -c $< -o $@
 
-$(OBJ_DIR)/runtime.cpp.o: $(SRC_DIR)/runtime.cpp $(HEADERS)
+# Per-kernel register/LDS table of the kernels above, read from their own code
+# objects, compiled into runtime.cpp (mb_kernel_attrs_get).
+KERNEL_OBJS := $(filter-out $(OBJ_DIR)/runtime.cpp.o,$(HIP_OBJS))
+RESOURCES   := build/kernel_resources.inc
+
+$(RESOURCES): $(KERNEL_OBJS) metalbench_amd/kernel_resources.py
+	python3 metalbench_amd/kernel_resources.py $(KERNEL_OBJS) > $@.tmp
+	mv -f $@.tmp $@
+
+$(OBJ_DIR)/runtime.cpp.o: $(SRC_DIR)/runtime.cpp $(HEADERS) $(RESOURCES)
 	@mkdir -p $(OBJ_DIR)
-	$(HIPCC) $(HIPFLAGS) -x hip -c $< -o $@
+	$(HIPCC) $(HIPFLAGS) -Ibuild -x hip -c $< -o $@
 
 $(LIB): $(HIP_OBJS)
 	@mkdir -p $(dir $@)

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MBHIP_ABI_VERSION 1
+#define MBHIP_ABI_VERSION 2
 
 /* ---- status codes ------------------------------------------------------- */
 #define MB_OK             0
@@ -122,7 +122,9 @@ typedef struct mb_device_info {
 
 /* Kernel attributes; replaces the PSO's staticThreadgroupMemoryLength and
  * maxTotalThreadsPerThreadgroup (reference metal/scripts/main.mm:119-123,
- * 186-192).  For multi-kernel entries they describe the dominant kernel. */
+ * 186-192).  For multi-kernel entries they describe the dominant kernel.
+ * The register counts come from this library's own code objects (metadata
+ * note and kernel descriptor, read at build time); -1 if not found. */
 typedef struct mb_kernel_attrs {
     uint64_t static_lds_bytes;
     int32_t  max_threads_per_block;
@@ -130,6 +132,10 @@ typedef struct mb_kernel_attrs {
     uint64_t private_bytes;      /* per-thread scratch (spills); 0 is good */
     int32_t  n_parts;            /* kernels launched per dispatch       */
     int32_t  dominant_part;
+    int32_t  arch_vgprs;         /* architectural VGPRs per lane        */
+    int32_t  agprs;              /* accumulation VGPRs (MFMA) per lane  */
+    int32_t  sgprs;              /* scalar registers per wave           */
+    int32_t  waves_per_simd;     /* occupancy the registers and LDS allow (1..8) */
 } mb_kernel_attrs;
 
 /* ---- lifecycle ----------------------------------------------------------- */

@@ -8,14 +8,15 @@
 //
 // gfx950 design (MFMA bound: 2*M*N*K flops vs 2*(MK+KN+MN) bytes):
 //  * workgroup tile 256x256, 4 waves in a 2x2 grid, each wave a 128x128
-//    sub-tile = 4x4 v_mfma_f32_32x32x16_bf16 accumulators (256 fp32 per
-//    lane, held in AccVGPRs); one workgroup per CU, 1024 tiles at 8192^3 =
-//    exactly four rounds of 256 CUs;
+//    sub-tile (256 fp32 accumulators per lane, held in AccVGPRs); one
+//    workgroup per CU, 1024 tiles at 8192^3 = exactly four rounds of 256 CUs;
 //  * full tiles (the large_mm shape) take gemm_bf16_full_kernel further down:
-//    both operands go global -> LDS by DMA into a four-stage ring (no staging
-//    registers, no LDS store instructions) and B is transposed by the LDS
-//    reads (ds_read_b64_tr_b16);
-//  * other shapes take gemm_bf16_kernel, BK = 64 with an LDS double buffer:
+//    8 x 8 v_mfma_f32_16x16x32_bf16 per wave and 32-deep k stage, both
+//    operands global -> LDS by DMA into a four-stage ring (no staging
+//    registers, no LDS store instructions), B transposed by the LDS reads
+//    (ds_read_b64_tr_b16);
+//  * other shapes take gemm_bf16_kernel (4 x 4 v_mfma_f32_32x32x16_bf16 per
+//    wave), BK = 64 with an LDS double buffer:
 //    both operands stored K-contiguous, row pitch 72 bf16 (144 B), 2 x 2 x
 //    36 KB = 144 KB of the 160 KB.  With that pitch the MFMA operand reads
 //    (ds_read_b128 of 16 consecutive rows) and both store patterns below
@@ -221,30 +222,32 @@ void gemm_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
 // Both operands go global -> LDS by DMA (buffer_load ... lds): no staging
 // registers and no LDS store instructions, whose VGPR reads stall the MFMA
 // issue.  The LDS holds a ring of four 32-deep k stages (A 16 KB + B 16 KB
-// each), so a stage's DMAs are issued three stages before its MFMAs:
+// each), so a stage's DMAs are issued three stages before its MFMAs (a
+// two-stage lead, or a five-buffer ring of 160 KB, measured slower):
 //  * A [256 rows][32 k], 64-byte rows; chunk c (8 k) of row r sits in slot
-//    c ^ ((r / 4) % 4).  A ds_read_b128 serves 16 lanes = 16 consecutive
-//    rows per LDS cycle, whose 16-byte bank groups 4 (r % 4) + slot are then
-//    all distinct;
+//    c ^ ((r / 4) % 4).  The 16x16x32 A operand of row block i is one
+//    ds_read_b128: lane l reads row 16 i + l%16, chunk l/16; each 16 lanes
+//    (16 consecutive rows, one chunk) hit 16 distinct 16-byte bank groups;
 //  * B [32 k][256 n] row-major as in HBM, 512-byte rows; chunk c (8 n) of
-//    k-row r sits in slot c ^ (4 (r % 4)).  The MFMA B operand (8
-//    consecutive k of one column) is two ds_read_b64_tr_b16: in each 16-lane
-//    group lane s points at k-row k0 + s/4, columns n0 + 4 (s % 4) .. +3,
-//    and lane s receives column n0 + s, k-rows k0 .. k0+3;
+//    k-row r sits in slot c ^ f(r), f(r) = 4 (r % 4) ^ 2 ((r / 8) % 2).  The
+//    B operand (8 consecutive k of one column) is two ds_read_b64_tr_b16: in
+//    16-lane group g lane s points at k-row 8 g + 4 q + s/4, columns
+//    n0 + 4 (s % 4) .. +3, and receives column n0 + s, those 4 k-rows.  The
+//    ^ 2 ((r/8) % 2) term puts k-rows r and r + 8 (groups 0 and 1, read in
+//    the same LDS cycle) in different banks;
 //  * each DMA instruction writes a wave's 64 x 16 B contiguously, so lane l
 //    fetches the global chunk that its slot holds.
-// Stage s (buffer s % 4): k step 0 reads the operands of k step 1 under its
-// 16 MFMAs; k step 1 waits for this wave's DMAs of stage s+1, passes an
-// LDS barrier (every wave has then read all of stage s, and every wave's
-// stage s+1 DMAs have landed), refills buffer s % 4 with stage s+4 and reads
-// stage s+1's first operands under its 16 MFMAs.  The operands of k step 1
-// are already in registers when its barrier passes, and the DMAs have three
-// stages (~1.5 us) to land.
-// Measured on MI355X against the previous design (both operands staged in
-// registers two stages ahead, B transposed with v_perm_b32, ds_write_b128
-// into a padded double buffer): MFMA busy 73 % -> 85 % of the kernel's
-// cycles and 6-10 % less time per 8192^3 launch.  The LDS store instructions
-// were what stalled the MFMA issue (removing only them gave 91 %).
+// The MFMA is v_mfma_f32_16x16x32_bf16, not 32x32x16: on random bf16 data
+// the chip is power-limited, and a register-only loop of 16x16x32 sustains
+// 1.90-2.12 PF against 1.50-1.85 PF for 32x32x16 at the same power.  In the
+// GEMM it took an 8192^3 launch from 791-816 us to 756-773 us on the same box
+// (bit-identical output: every k32 sum rounds to the same bf16).
+// Stage s (buffer s % 4, operands in register set s % 2): rows 0-3 of the
+// wave's 8 x 8 blocks (32 MFMAs); wait for this wave's DMAs of stage s+1 and
+// pass one LDS barrier (every wave read stage s during stage s-1, and every
+// wave's stage s+1 DMAs have landed); refill buffer s % 4 with stage s+4 and
+// read all of stage s+1's operands into the other register set under rows
+// 4-7 (32 MFMAs).
 constexpr int KS = 32;                    // k per LDS stage
 constexpr int AROWB = KS * 2;             // bytes per A row in LDS
 constexpr int BROWB = BN * 2;             // bytes per B k-row in LDS
@@ -255,6 +258,8 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
 
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(256, 1)
 void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
@@ -281,17 +286,18 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
     // A DMA: instruction i of wave w fills rows 64 w + 16 i + l/4, slot l%4,
     // which holds chunk (l%4) ^ ((l/16) % 4).
     const uint32_t a_voff = ((lane >> 2) * K + 8 * ((lane & 3) ^ ((lane >> 4) & 3))) * 2;
-    // B DMA: instruction i of wave w fills k-rows 8 w + 2 i + l/32, slot l%32,
-    // which holds chunk (l%32) ^ (4 ((2 i + l/32) % 4)).
+    // B DMA: instruction i of wave w fills k-rows r = 8 w + 2 i + l/32, slot
+    // l%32, which holds chunk (l%32) ^ f(r), f(r) = 4 (r % 4) ^ 2 ((r / 8) % 2):
+    // k-rows r and r + 8, read by the same half-wave of ds_read_b64_tr_b16,
+    // land in different banks.
     const uint32_t b_r = lane >> 5;
-    const uint32_t b_voff0 = (b_r * N + 8 * ((lane & 31) ^ (4 * b_r))) * 2;
-    const uint32_t b_voff1 = (b_r * N + 8 * ((lane & 31) ^ (4 * (2 + b_r)))) * 2;
-    // LDS byte addresses of the ring buffers and of this wave's DMA targets.
+    const uint32_t bx = 2 * (wave & 1);
+    const uint32_t b_voff0 = (b_r * N + 8 * ((lane & 31) ^ (4 * b_r) ^ bx)) * 2;
+    const uint32_t b_voff1 = (b_r * N + 8 * ((lane & 31) ^ (4 * (2 + b_r)) ^ bx)) * 2;
     const uint32_t ring[4] = {(uint32_t)(uintptr_t)(lds_void_t*)L0, (uint32_t)(uintptr_t)(lds_void_t*)L1,
                               (uint32_t)(uintptr_t)(lds_void_t*)L2, (uint32_t)(uintptr_t)(lds_void_t*)L3};
     const uint32_t a_dst = 64 * wave * AROWB, b_dst = STAGE_A * 2 + 8 * wave * BROWB;
     const uint32_t a_src = (m0 + 64 * wave) * K * 2, b_src = (8 * wave * N + n0) * 2;
-    // DMA instructions i (A) and i (B) of stage k0 into ring buffer rb.
     auto dma_part = [&](int rb, uint32_t k0, int i) {
         dma16(ars, ring[rb] + a_dst + 16 * i * AROWB, a_voff, a_src + (16 * i * K + k0) * 2);
         dma16(brs, ring[rb] + b_dst + 2 * i * BROWB, (i & 1) ? b_voff1 : b_voff0,
@@ -302,98 +308,95 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
         for (int i = 0; i < 4; ++i) dma_part(rb, k0, i);
     };
 
-    f32x16 acc[4][4];
+    f32x4 acc[8][8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{};
 
-    const uint32_t li = lane & 31, lh = lane >> 5;
-    // A operand (i, kk): row wm*128 + 32 i + li, chunk 2 kk + lh, in slot
-    // chunk ^ ((li/4) % 4).
-    const uint32_t a_row = (wm * 128 + li) * AROWB, a_sw = (li >> 2) & 3;
-    // B operand (j, kk), half q: k-row 16 kk + 4 q + tr_row, column
-    // tr_col + 32 j (tr_row % 4 = (l/4) % 4 for every kk, q).
-    const uint32_t tr_row = 8 * lh + ((lane & 15) >> 2);
-    const uint32_t tr_col = wn * 128 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-    uint32_t b_off[4];
+    // 16x16x32 operands.  A (i): lane l holds row wm*128 + 16 i + l%16,
+    // k octet l/16 (chunk l/16 of the row, in slot chunk ^ ((row/4) % 4)).
+    const uint32_t g = lane >> 4, t = lane & 15;
+    const uint32_t a_row = (wm * 128 + t) * AROWB, a_slot = 16 * (g ^ ((t >> 2) & 3));
+    // B (j): lane l needs column wn*128 + 16 j + l%16, k = 8 (l/16) .. +7:
+    // two ds_read_b64_tr_b16 (k-rows 8g + 4q + t/4, columns 4 (t%4) .. +3 of
+    // the 16-column block), each returning 4 k of column t.
+    uint32_t b_off[8][2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t c = tr_col + 32 * j;
-        b_off[j] = tr_row * BROWB + 16 * ((c >> 3) ^ (4 * (tr_row & 3))) + 2 * (c & 7);
-    }
-    auto b_at = [&](const uint8_t* bs, int j, int kk) {
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const uint32_t r = 8 * g + 4 * q + (t >> 2);
+            const uint32_t c = wn * 128 + 16 * j + 4 * (t & 3);
+            const uint32_t f = 4 * (r & 3) ^ 2 * ((r >> 3) & 1);
+            b_off[j][q] = r * BROWB + 16 * ((c >> 3) ^ f) + 2 * (c & 7);
+        }
+    auto b_at = [&](const uint8_t* bs, int j) {
         u32x2 h[2];
 #pragma unroll
         for (int q = 0; q < 2; ++q)
             h[q] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_s16x4_t*)(bs + b_off[j] + (16 * kk + 4 * q) * BROWB)));
+                (lds_s16x4_t*)(bs + b_off[j][q])));
         return __builtin_bit_cast(bf16x8, u32x4{h[0][0], h[0][1], h[1][0], h[1][1]});
     };
-    bf16x8 a[2][4], b[2][4];
-    auto read_ops = [&](const uint16_t* buf, int kk, int c) {   // order a0, b0..b3, a1..a3
-        const uint8_t* as = reinterpret_cast<const uint8_t*>(buf) + a_row;
-        const uint8_t* bs = reinterpret_cast<const uint8_t*>(buf + STAGE_A);
-        auto a_at = [&](int i) {
-            return *reinterpret_cast<const bf16x8*>(as + 32 * i * AROWB + 16 * ((2 * kk + lh) ^ a_sw));
-        };
-        a[c][0] = a_at(0);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) b[c][j] = b_at(bs, j, kk);
-#pragma unroll
-        for (int i = 1; i < 4; ++i) a[c][i] = a_at(i);
+    auto a_at = [&](const uint8_t* as, int i) {
+        return *reinterpret_cast<const bf16x8*>(as + 16 * i * AROWB + a_slot);
     };
-    // Snake order over j (odd i run j backwards), so consecutive MFMAs of a
-    // k step share an operand register: 0.3-0.5 % faster at the power-limited
-    // clock.
-    auto mfmas = [&](int c) {
+    bf16x8 a[2][8], b[2][8];
+    // The MFMAs are inline asm with the accumulators pinned to AccVGPRs
+    // ("+a"): with 64 four-register accumulators the register allocator
+    // otherwise shuttles them between AccVGPRs and VGPRs every iteration.
+    // The wait-count pass sees the asm operands (it waits for the operand
+    // reads); the one hazard it cannot see -- reading an accumulator right
+    // after the MFMA that writes it -- is padded before the epilogue.
+    auto mfma = [&](int c, int i, int jj) {
+        const int j = (i & 1) ? 7 - jj : jj;
+        asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                     : "+a"(acc[i][j]) : "v"(a[c][i]), "v"(b[c][j]));
+    };
+    // Stage s on ring buffer rc, operands in register set c: rows 0-3 (32
+    // MFMAs); wait for this wave's DMAs of stage s+1 and pass one LDS barrier
+    // (every wave read stage s during stage s-1, and stage s+1 has landed);
+    // refill buffer rc with stage s+4 and read stage s+1's operands into set
+    // c^1 under rows 4-7 (32 MFMAs).
+    auto stage = [&](int rc, int c, const uint16_t* nxt, uint32_t kdma) {
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const int j = (i & 1) ? 3 - jj : jj;
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[c][i], b[c][j], acc[i][j], 0, 0, 0);
-            }
-    };
-    // One stage on ring buffer rc (pointer cur); `kdma` is the k of the stage
-    // that refills it.  k step 1 is four chunks, each: two DMAs, three
-    // operand reads of the next stage (a_q, b_q), four MFMAs (row block q).
-    auto stage = [&](int rc, const uint16_t* cur, const uint16_t* nxt, uint32_t kdma) {
-        __builtin_amdgcn_sched_barrier(0);
-        read_ops(cur, 1, 1);
-        mfmas(0);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {   // 16 MFMA, 12 operand reads
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // DS read
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
-        }
+            for (int jj = 0; jj < 8; ++jj) mfma(c, i, jj);
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(0x4F70);   // vmcnt(16): stages s+2, s+3 may be in flight
         lds_barrier();
         __builtin_amdgcn_sched_barrier(0);
         const uint8_t* nas = reinterpret_cast<const uint8_t*>(nxt) + a_row;
         const uint8_t* nbs = reinterpret_cast<const uint8_t*>(nxt + STAGE_A);
+        // Reads in the order the next stage consumes them: its first row
+        // needs A0 and every B, the later rows one A each.
+        // row 4: B0 B1 A0 B2   row 5: B3 B4 A1 B5   row 6: B6 B7 A2 A3
+        // row 7: A4 A5 A6 A7 (a B is two reads, an A one)
+        auto rd = [&](int u) {
+            if (u < 8) b[c ^ 1][u] = b_at(nbs, u);
+            else a[c ^ 1][u - 8] = a_at(nas, u - 8);
+        };
+        constexpr int order[4][4] = {{0, 1, 8, 2}, {3, 4, 9, 5}, {6, 7, 10, 11}, {12, 13, 14, 15}};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             dma_part(rc, kdma, q);
-            __builtin_amdgcn_sched_barrier(0);
-            a[0][q] = *reinterpret_cast<const bf16x8*>(nas + 32 * q * AROWB + 16 * (lh ^ a_sw));
-            b[0][q] = b_at(nbs, q, 0);
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const int j = (q & 1) ? 3 - jj : jj;
-                acc[q][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1][q], b[1][j], acc[q][j], 0, 0, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // DS read
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // 2 MFMA
-            __builtin_amdgcn_sched_barrier(0);
+            mfma(c, 4 + q, 0);
+            rd(order[q][0]);
+            mfma(c, 4 + q, 1);
+            mfma(c, 4 + q, 2);
+            rd(order[q][1]);
+            mfma(c, 4 + q, 3);
+            rd(order[q][2]);
+            mfma(c, 4 + q, 4);
+            mfma(c, 4 + q, 5);
+            rd(order[q][3]);
+            mfma(c, 4 + q, 6);
+            mfma(c, 4 + q, 7);
         }
+        __builtin_amdgcn_sched_barrier(0);
     };
 
     dma(0, 0);
@@ -402,33 +405,34 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
     dma(3, 3 * KS);
     __builtin_amdgcn_s_waitcnt(0x4F78);   // vmcnt(24): stage 0 has landed
     lds_barrier();
-    read_ops(L0, 0, 0);
-    // nstages % 4 == 0, so the body is straight-line; past the last stage the
-    // clamped DMAs re-read it into buffers that are never read again.
+    {
+        const uint8_t* as = reinterpret_cast<const uint8_t*>(L0) + a_row;
+        const uint8_t* bs = reinterpret_cast<const uint8_t*>(L0 + STAGE_A);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { a[0][i] = a_at(as, i); b[0][i] = b_at(bs, i); }
+    }
     for (uint32_t s = 0; s < nstages; s += 4) {
-        stage(0, L0, L1, min((s + 4) * KS, last_k0));
-        stage(1, L1, L2, min((s + 5) * KS, last_k0));
-        stage(2, L2, L3, min((s + 6) * KS, last_k0));
-        stage(3, L3, L0, min((s + 7) * KS, last_k0));
+        stage(0, 0, L1, min((s + 4) * KS, last_k0));
+        stage(1, 1, L2, min((s + 5) * KS, last_k0));
+        stage(2, 0, L3, min((s + 6) * KS, last_k0));
+        stage(3, 1, L0, min((s + 7) * KS, last_k0));
     }
     __builtin_amdgcn_s_waitcnt(0);   // no DMA may still target LDS
+    // the last MFMAs' results must be written before they are read
+    asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory");
 
-    // Epilogue through LDS: each wave converts its 128 x 128 tile to bf16
-    // (hardware round-to-nearest-even convert), writes it row-major into its
-    // own 32 KB buffer of the ring, and streams it out as 16-byte row chunks
-    // (a wave store instruction covers four 256-byte row segments).
-    // Lane l, reg r of 32x32 block (i, j): row 32 i + 8 (r/4) + 4 (l/32) + r%4,
-    // column 32 j + l%32.
-    lds_barrier();   // every wave is done reading the operand buffers
+    // Epilogue through LDS: lane l, reg r of 16x16 block (i, j) is row
+    // 16 i + 4 (l/16) + r, column 16 j + l%16 of the wave's 128 x 128 tile.
+    lds_barrier();
     uint16_t* ct = wave == 0 ? L0 : wave == 1 ? L1 : wave == 2 ? L2 : L3;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 8; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const uint32_t row = 32 * i + 8 * (r >> 2) + 4 * lh + (r & 3);
-                ct[row * 128 + 32 * j + li] = __builtin_bit_cast(uint16_t, (__bf16)acc[i][j][r]);
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t row = 16 * i + 4 * g + r;
+                ct[row * 128 + 16 * j + t] = __builtin_bit_cast(uint16_t, (__bf16)acc[i][j][r]);
             }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_wave_barrier();

@@ -108,6 +108,38 @@ void* library_flush_buffer(size_t* bytes) {
     return g.flush;
 }
 
+// ---- register / LDS usage of the built kernels --------------------------------------
+struct KernelResources {
+    const char* name;   // mangled kernel symbol
+    int arch_vgprs, agprs, sgprs, lds_bytes, private_bytes;
+};
+static const KernelResources k_resources[] = {
+#include "kernel_resources.inc"
+    {nullptr, 0, 0, 0, 0, 0}};
+
+static const KernelResources* resources_of(const char* name) {
+    if (!name) return nullptr;
+    for (const KernelResources* r = k_resources; r->name; ++r)
+        if (strcmp(r->name, name) == 0) return r;
+    return nullptr;
+}
+
+// Waves per SIMD that a workgroup of `threads` lanes can keep resident on
+// gfx950: 512 unified VGPRs per lane per SIMD (ArchVGPRs then AGPRs, each
+// wave's allocation rounded up to a granule of 8, ArchVGPRs to 4 first), 160
+// KB of LDS per CU shared by its 4 SIMDs, at most 8 waves per SIMD.
+static int waves_per_simd(int arch_vgprs, int agprs, uint64_t lds_bytes, int threads) {
+    const int arch = (arch_vgprs + 3) & ~3;
+    const int total = std::max(8, (arch + agprs + 7) & ~7);
+    int waves = std::min(8, 512 / total);
+    const int waves_per_group = std::max(1, (threads + 63) / 64);
+    if (lds_bytes > 0) {
+        const int groups = (int)std::min<uint64_t>(64, (160u << 10) / lds_bytes);
+        waves = std::min(waves, std::max(0, groups * waves_per_group / 4));
+    }
+    return std::max(waves, 1);
+}
+
 // ---- kernel registry ------------------------------------------------------------
 static std::vector<KernelEntry>& table() {
     static std::vector<KernelEntry> t;
@@ -322,6 +354,14 @@ int mb_kernel_attrs_get(int id, mb_kernel_attrs* out) {
     out->private_bytes = a.localSizeBytes;
     out->n_parts = t[id].n_parts;
     out->dominant_part = 0;
+    out->arch_vgprs = out->agprs = out->sgprs = out->waves_per_simd = -1;
+    if (const KernelResources* r = resources_of(hipKernelNameRefByPtr(t[id].dominant_kernel, nullptr))) {
+        out->arch_vgprs = r->arch_vgprs;
+        out->agprs = r->agprs;
+        out->sgprs = r->sgprs;
+        out->waves_per_simd = waves_per_simd(r->arch_vgprs, r->agprs, a.sharedSizeBytes,
+                                             a.maxThreadsPerBlock);
+    }
     return MB_OK;
 }
 

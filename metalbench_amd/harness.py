@@ -87,6 +87,8 @@ def _run_native(b, inputs, warmup, iters, flags=native.RUN_SYNC_EACH):
     k_t["tg_static_mem_bytes"] = attrs["static_lds_bytes"]
     k_t["pso_max_threads_per_tg"] = attrs["max_threads_per_block"]
     k_t["vgprs"] = attrs["num_regs"]
+    for key in ("arch_vgprs", "agprs", "sgprs", "waves_per_simd"):
+        k_t[key] = attrs[key]
     k_t["hip_device"] = H.chip_info()["name"]
     del d_in, d_out
     return k_t, outs
@@ -178,6 +180,7 @@ def evaluate(name, *, seed, warmup, iters, dry_run=False, profile=False, solo=No
         "metal_device": k_t.get("hip_device", "unknown"),
         "tg_static_mem_bytes": k_t.get("tg_static_mem_bytes"),
         "pso_max_threads_per_tg": k_t.get("pso_max_threads_per_tg"),
+        "registers": {k: k_t.get(k) for k in ("arch_vgprs", "agprs", "sgprs", "waves_per_simd")},
         "correct": correct,
         "metrics": metrics,
         "speedup": speedup,
@@ -374,8 +377,13 @@ def _print_report(result, target, score):
           f"{chip['cpu_cores']} CPU / {chip['gpu_cores']} GPU / "
           f"{chip['ram_bytes']/1e9:.0f} GB")
     if result.get("tg_static_mem_bytes") is not None:
+        regs = result.get("registers") or {}
+        extra = ""
+        if (regs.get("arch_vgprs") or -1) >= 0:
+            extra = (f"  vgpr={regs['arch_vgprs']} agpr={regs['agprs']} sgpr={regs['sgprs']}"
+                     f"  waves/simd={regs['waves_per_simd']}")
         print(f"  occupancy   : tg_mem={_bytes_human(result['tg_static_mem_bytes'])}  "
-              f"max_thr/tg={result['pso_max_threads_per_tg']}")
+              f"max_thr/tg={result['pso_max_threads_per_tg']}{extra}")
     print()
     status = "✓ correct " if result["correct"] else "✗ INCORRECT"
     max_err = max((o["max_err"] for o in outs), default=0.0)

@@ -74,7 +74,8 @@ class MbDeviceInfo(Structure):
 class MbKernelAttrs(Structure):
     _fields_ = [("static_lds_bytes", c_uint64), ("max_threads_per_block", c_int32),
                 ("num_regs", c_int32), ("private_bytes", c_uint64), ("n_parts", c_int32),
-                ("dominant_part", c_int32)]
+                ("dominant_part", c_int32), ("arch_vgprs", c_int32), ("agprs", c_int32),
+                ("sgprs", c_int32), ("waves_per_simd", c_int32)]
 
 
 class MbDecoderStepArgs(Structure):

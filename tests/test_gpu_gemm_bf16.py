@@ -12,6 +12,7 @@ import torch
 
 import oracle
 from gpu_util import assert_close, launch, ptr, run_registry, seeded
+from metalbench_amd import native
 
 pytestmark = pytest.mark.gpu
 
@@ -68,3 +69,16 @@ def test_large_mm_registry_config_sampled(mb):
     got = outs[0][rows]
     assert_close(oracle.as_f64(got), exact, b.rtol, b.atol, "large_mm sample")
     _check_rounding(_bits(got), exact, "large_mm sample")
+
+
+def test_kernel_attrs_report_register_split(mb):
+    """mb_kernel_attrs_get reports the ArchVGPR / AGPR / SGPR counts of the
+    kernel's own code object: the bf16 GEMM keeps its 4 x 4 32x32 accumulator
+    tiles (256 per lane) in AGPRs, so one wave per SIMD fits."""
+    a = native.kernel_attrs(native.kernel_find("large_matmul_bf16"))
+    assert a["agprs"] == 256 and 0 < a["arch_vgprs"] <= 256, a
+    assert a["arch_vgprs"] + a["agprs"] <= 512 and a["sgprs"] > 0
+    assert a["waves_per_simd"] == 1 and a["static_lds_bytes"] == 131072
+    for name in native.kernel_names():
+        attrs = native.kernel_attrs(native.kernel_find(name))
+        assert attrs["arch_vgprs"] > 0 and 1 <= attrs["waves_per_simd"] <= 8, (name, attrs)

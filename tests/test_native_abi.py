@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_struct_layouts_match():
     lib = native.load()
-    assert lib.mb_abi_version() == 1
+    assert lib.mb_abi_version() == 2
     for which, S in native.STRUCTS.items():
         assert lib.mb_abi_struct_size(which) == ctypes.sizeof(S), S.__name__
     assert lib.mb_abi_struct_size(99) == -1
