@@ -211,6 +211,10 @@ void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt
 //    MFMAs; before group 1 the wave waits for its DMAs of stage s+1, passes an
 //    LDS barrier, refills slot s % NBUF with stage s+NBUF and reads stage
 //    s+1's first operands under group 1's MFMAs.
+// Tiles are taken in XCD-aware order (each XCD a contiguous pixel range, 4
+// whole images at this shape), so the rows a filter's halo shares between
+// neighbouring tiles are fetched into one L2: FETCH_SIZE per launch fell from
+// 3.17x to 1.04x the input + weight bytes, at unchanged time.
 // Measured on the 32x56x56x64 -> 64 shape, alternated on one box: 90.2-91.3
 // us against 95.2-96.1 us for the register-staged version of this path
 // (conv2d_f32_kernel's layout with buffer loads); 64-pixel tiles (WMS = 2)
@@ -234,8 +238,13 @@ void conv2d_f32_dma_kernel(const float* __restrict__ X, const float* __restrict_
     const uint32_t lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wk = wave / (2 * WMS), wm = (wave >> 1) % WMS, wn = wave & 1;
-    const uint32_t tm = blockIdx.x / tiles_n;
-    const uint32_t tn = blockIdx.x - tm * tiles_n;
+    // XCD-aware order: hardware block b runs on XCD b % 8, so XCD x gets the
+    // contiguous logical range [x G/8, (x+1) G/8) of the G tiles (pixel
+    // order): tiles that share input rows (the filter's halo) share an L2.
+    uint32_t lb = blockIdx.x;
+    if ((gridDim.x & 7) == 0) lb = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+    const uint32_t tm = lb / tiles_n;
+    const uint32_t tn = lb - tm * tiles_n;
     const uint32_t m0 = tm * BMT, n0 = tn * BN;
     const uint32_t nstages = (sh.k + BK - 1) / BK;
 
