@@ -597,6 +597,7 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
 // together, so the merge costs one memory round trip.
 
 constexpr int AKEYS = 64;                 // keys per workgroup iteration
+constexpr int AR = 2;                     // 64-key blocks in flight per workgroup
 constexpr int APITCH = DH + 4;            // floats per (split, head) partial: o[DH], m, l, pad
 constexpr int QP = DH + 8;                // LDS pitch (bf16) of a query row
 constexpr float NEG_BIG = -1.0e30f;       // "no key yet": finite, so max/exp never see inf - inf
@@ -610,7 +611,11 @@ template <int GT>
 __global__ __launch_bounds__(256)
 void attention_kernel(StepParams p) {
     __shared__ uint16_t qs[16][QP];        // q rows of this kv head (rows past G zero)
-    __shared__ float xp[4][16][16];       // per wave: p[key][head] of the current block
+    // per wave: p[key][head] of the current block.  Row pitch 20 floats: the
+    // store of lane (j, grp), row 4 grp + r, lands in bank 16 grp + 20 r + j,
+    // so the 64 lanes hit 64 banks (with a pitch of 16 the four grp rows were
+    // 64 floats apart: a 4-way conflict on every store).
+    __shared__ __attribute__((aligned(16))) float xp[4][16][20];
     __shared__ float xa[4][4][16];        // per wave: rescale factor of each head (row 0 read)
     __shared__ float wo[4][GT][DH];       // per wave: o after the key loop
     __shared__ float wm[4][GT], wl[4][GT];
@@ -658,9 +663,12 @@ void attention_kernel(StepParams p) {
     const uint32_t qh = tid / (DH / 8), qc = tid % (DH / 8);
     const u32x4 qv = *reinterpret_cast<const u32x4*>(
         p.q + (size_t)b * p.d + (kvh * G + (qh < G ? qh : 0)) * DH + 8 * qc);
-    KVBlock ba, bb;
-    load(ba, 0);
-    __builtin_amdgcn_sched_barrier(0);
+    KVBlock kv[AR];
+#pragma unroll
+    for (int u = 0; u < AR - 1; ++u) {
+        load(kv[u], u);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     *reinterpret_cast<u32x4*>(&qs[qh][8 * qc]) = qh < G ? qv : u32x4{};
     __syncthreads();
 
@@ -726,17 +734,19 @@ void attention_kernel(StepParams p) {
         __builtin_amdgcn_wave_barrier();
     };
 
-    // sched_barrier pins the order: a block's loads are issued right after the
-    // previous block's compute, so exactly two blocks are ever live.
-    for (uint32_t t = 0; t < nblk; t += 2) {
-        __builtin_amdgcn_sched_barrier(0);
-        load(bb, t + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(ba, t);
-        __builtin_amdgcn_sched_barrier(0);
-        load(ba, t + 2);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(bb, t + 1);
+    // A ring of AR blocks: block t + AR - 1 is issued right before block t is
+    // computed, so AR blocks (AR x 32 KB per workgroup) are in flight.  Four
+    // in flight measured 1.5 us slower than two at the BASELINE shape (more
+    // concurrent streams per CU, less DRAM page locality).  sched_barrier
+    // pins the order.
+    for (uint32_t t = 0; t < nblk; t += AR) {
+#pragma unroll
+        for (int u = 0; u < AR; ++u) {
+            __builtin_amdgcn_sched_barrier(0);
+            load(kv[(u + AR - 1) % AR], t + u + AR - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(kv[u], t + u);
+        }
     }
 
     // ---- fold each wave's key groups, then the four waves ----
@@ -913,15 +923,16 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
     pl->nqkv = D + 2 * a->n_kv_heads * DH;
     pl->g = a->n_heads / a->n_kv_heads;
     {   // attention: about one workgroup per CU (fewer, longer streams read HBM
-        // faster than several per CU); splits of a multiple of 128 keys (an even
-        // number of 64-key iterations, as the loop is unrolled by two)
+        // faster than several per CU); splits of a multiple of AR x 64 keys
+        // (the loop runs AR 64-key iterations per trip)
         const uint32_t pairs = B * a->n_kv_heads;
         const uint32_t want = std::max(1u, cdiv(PLAN_CUS, pairs));
-        const uint32_t nmax = std::max(1u, cdiv(a->cache_len, 2 * AKEYS));
+        const uint32_t nmax = std::max(1u, cdiv(a->cache_len, AR * AKEYS));
         const uint32_t per = cdiv(std::max(a->cache_len, 1u), std::min(want, nmax));
-        pl->split_keys = cdiv(per, 2 * AKEYS) * 2 * AKEYS;
+        pl->split_keys = cdiv(per, AR * AKEYS) * AR * AKEYS;
         pl->nsplit = std::max(1u, cdiv(a->cache_len, pl->split_keys));
-        if ((uint64_t)(pl->split_keys + 2 * AKEYS) * DH * 2 > 0xffffffffull)
+        // the ring's loads run up to AR - 1 blocks past the split
+        if ((uint64_t)(pl->split_keys + AR * AKEYS) * DH * 2 > 0xffffffffull)
             return fail(MB_E_ARG, "decoder step: cache_len %u too large", a->cache_len);
     }
     pl->tiles[EPI_QKV] = pl->nqkv / BN;
