@@ -9,7 +9,9 @@ decoder decode step ("decoder block us/step"); the other four
 configurations (sqr_mm, transpose_2d, conv2d, large_mm) are timed the same way
 and reported under "kernels", each with its own roofline fraction.
 
-Timing: W untimed steps, then exactly K steps launched back to back with no
+Timing: first the workload's own launches keep the GPU busy for --settle-ms
+(100 ms; an idle MI355X needs ~30 ms of MFMA work to reach its working
+clock), then W untimed steps, then exactly K steps launched back to back with no
 events in the stream, bracketed by torch.cuda.synchronize() on both sides;
 ms_per_step is the host wall clock of the K steps / K.  The HBM-bound
 workloads (decoder step, transpose) are timed cold: each step uses the next of
@@ -222,6 +224,33 @@ def _async_launcher(name, b, copies_in, copies_out):
     return None
 
 
+def _settle(launch_n, ms: float) -> float:
+    """Keep the GPU busy with the workload's own launches for `ms` of wall time
+    (batches of launch_n(count), doubled until one takes >= 5 ms, each followed
+    by a synchronize); returns the time spent.
+
+    An idle MI355X reaches its working clock only after ~25-30 ms of
+    continuous MFMA work: right after an idle second, conv2d launches went
+    150 -> 101 -> 93 -> 88 -> 85 -> 83 us over the first 30 ms and the 8192^3
+    bf16 GEMM 1306 -> 964 -> 892 -> 832 -> 823 us, flat after that; the
+    HBM-bound decode step was flat from its second millisecond.  W warmup
+    launches of a 21 us kernel end long before that, so without this the K
+    timed steps would measure the ramp."""
+    import torch
+
+    t0 = time.perf_counter()
+    batch = 1
+    while True:
+        t1 = time.perf_counter()
+        launch_n(batch)
+        torch.cuda.synchronize()
+        now = time.perf_counter()
+        if (now - t0) * 1e3 >= ms:
+            return (now - t0) * 1e3
+        if (now - t1) * 1e3 < 5.0:
+            batch *= 2
+
+
 def _mean_timing(runs: list) -> dict:
     """Average single-iteration mb_run timings (and their per-kernel parts)."""
     out = {"mean_ms": sum(r["mean_ms"] for r in runs) / len(runs)}
@@ -234,7 +263,7 @@ def _mean_timing(runs: list) -> dict:
     return out
 
 
-def _run_workload(name, steps, warmup, want_cpu):
+def _run_workload(name, steps, warmup, want_cpu, settle_ms):
     import ctypes
 
     import torch
@@ -270,6 +299,14 @@ def _run_workload(name, steps, warmup, want_cpu):
     kid = native.kernel_find(b.metal_function)
     launch = _async_launcher(name, b, copies_in, copies_out) if R > 1 else None
     torch.cuda.synchronize()
+    if launch:
+        def launch_n(count):
+            for i in range(count):
+                launch(i % R)
+    else:
+        def launch_n(count):
+            native.run(kid, bind_sets[0], 0, count, native.RUN_WALL_ONLY)
+    settled_ms = _settle(launch_n, settle_ms) if settle_ms > 0 else 0.0
     if warmup > 0:
         if launch:
             for i in range(warmup):
@@ -315,7 +352,8 @@ def _run_workload(name, steps, warmup, want_cpu):
            "gpu_median_ms": k_t["median_ms"], "gpu_mean_ms": k_t["mean_ms"],
            "roofline": _roofline(name, w, k_t, b.compute_dtype), "dtype": b.compute_dtype,
            "cache": (f"cold: {R} rotating copies of the working set" if R > 1
-                     else "warm: one set of buffers")}
+                     else "warm: one set of buffers"),
+           "clock_settle_ms": round(settled_ms, 1)}
     if k_t.get("parts"):
         rec["parts"] = [{"name": p["name"], "mean_us": p["mean_ms"] * 1e3,
                          **({"hbm_frac": w["parts"][p["name"]] / (p["mean_ms"] * 1e-3) / 1e9
@@ -336,6 +374,9 @@ def main(argv=None):
     ap.add_argument("--workload", default="llama_decoder_step")
     ap.add_argument("--only", action="store_true", help="skip the other configurations")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--settle-ms", type=float, default=100.0,
+                    help="busy time with the workload's own launches before the W warmup "
+                         "steps, so the timed steps run at the working clock (0: none)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run the 256 MiB copy kernel (counter calibration)")
     args = ap.parse_args(argv)
@@ -358,7 +399,8 @@ def main(argv=None):
     if args.only:
         others = []
     rank0 = True
-    head = _run_workload(args.workload, args.steps, args.warmup, not args.no_cpu_baseline)
+    head = _run_workload(args.workload, args.steps, args.warmup, not args.no_cpu_baseline,
+                         args.settle_ms)
     kernels = {}
     for n in others:
         from metalbench_amd import helpers as H
@@ -367,7 +409,8 @@ def main(argv=None):
             kernels[n] = {"status": "not built"}
             continue
         print(f"[bench] {n} ...", file=sys.stderr, flush=True)
-        kernels[n] = _run_workload(n, args.steps, args.warmup, not args.no_cpu_baseline)
+        kernels[n] = _run_workload(n, args.steps, args.warmup, not args.no_cpu_baseline,
+                                   args.settle_ms)
 
     from metalbench_amd import helpers as H
     meta = H.load_baseline(args.workload).meta
@@ -394,6 +437,7 @@ def main(argv=None):
         "config": config,
         "roofline": head["roofline"],
         "cache": head["cache"],
+        "clock_settle_ms": head["clock_settle_ms"],
         "cpu_baseline": head.get("cpu_baseline"),
         "gpu_mean_ms": head["gpu_mean_ms"],
         "parts": head.get("parts"),

@@ -242,12 +242,15 @@ void gemm_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
 // 1.90-2.12 PF against 1.50-1.85 PF for 32x32x16 at the same power.  In the
 // GEMM it took an 8192^3 launch from 791-816 us to 756-773 us on the same box
 // (bit-identical output: every k32 sum rounds to the same bf16).
-// Stage s (buffer s % 4, operands in register set s % 2): rows 0-3 of the
-// wave's 8 x 8 blocks (32 MFMAs); wait for this wave's DMAs of stage s+1 and
-// pass one LDS barrier (every wave read stage s during stage s-1, and every
-// wave's stage s+1 DMAs have landed); refill buffer s % 4 with stage s+4 and
-// read all of stage s+1's operands into the other register set under rows
-// 4-7 (32 MFMAs).
+// Stage s (buffer s % 4, operands in register set s % 2): wait for this
+// wave's DMAs of stage s+1 and pass one LDS barrier (every wave finished
+// reading stage s during stage s-1, and every wave's stage s+1 DMAs have
+// landed); then the wave's 8 x 8 blocks (64 MFMAs) run with the refill of
+// buffer s % 4 (stage s+4) and the reads of all of stage s+1's operands into
+// the other register set spread evenly under them.  With the barrier in the
+// middle of the stage instead (reads and DMAs under the second half only) the
+// LDS queue was oversubscribed in that half: 590 -> 561 us on zero operands,
+// 805-809 -> 794-802 us on random ones (power-limited), same box.
 constexpr int KS = 32;                    // k per LDS stage
 constexpr int AROWB = KS * 2;             // bytes per A row in LDS
 constexpr int BROWB = BN * 2;             // bytes per B k-row in LDS
@@ -354,47 +357,35 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
         asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
                      : "+a"(acc[i][j]) : "v"(a[c][i]), "v"(b[c][j]));
     };
-    // Stage s on ring buffer rc, operands in register set c: rows 0-3 (32
-    // MFMAs); wait for this wave's DMAs of stage s+1 and pass one LDS barrier
-    // (every wave read stage s during stage s-1, and stage s+1 has landed);
-    // refill buffer rc with stage s+4 and read stage s+1's operands into set
-    // c^1 under rows 4-7 (32 MFMAs).
+    // Stage s on ring buffer rc, operands in register set c.  Stage s+1's
+    // operands are read two per row of MFMAs in the order they are consumed
+    // (its first row needs every B and A0, the later rows one A each), and
+    // the refill goes out as one DMA part every other row.
     auto stage = [&](int rc, int c, const uint16_t* nxt, uint32_t kdma) {
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) mfma(c, i, jj);
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(0x4F70);   // vmcnt(16): stages s+2, s+3 may be in flight
         lds_barrier();
         __builtin_amdgcn_sched_barrier(0);
         const uint8_t* nas = reinterpret_cast<const uint8_t*>(nxt) + a_row;
         const uint8_t* nbs = reinterpret_cast<const uint8_t*>(nxt + STAGE_A);
-        // Reads in the order the next stage consumes them: its first row
-        // needs A0 and every B, the later rows one A each.
-        // row 4: B0 B1 A0 B2   row 5: B3 B4 A1 B5   row 6: B6 B7 A2 A3
-        // row 7: A4 A5 A6 A7 (a B is two reads, an A one)
+        // unit u < 8: B u (two transposing reads); u >= 8: A u-8 (one read)
         auto rd = [&](int u) {
             if (u < 8) b[c ^ 1][u] = b_at(nbs, u);
             else a[c ^ 1][u - 8] = a_at(nas, u - 8);
         };
-        constexpr int order[4][4] = {{0, 1, 8, 2}, {3, 4, 9, 5}, {6, 7, 10, 11}, {12, 13, 14, 15}};
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            dma_part(rc, kdma, q);
-            mfma(c, 4 + q, 0);
-            rd(order[q][0]);
-            mfma(c, 4 + q, 1);
-            mfma(c, 4 + q, 2);
-            rd(order[q][1]);
-            mfma(c, 4 + q, 3);
-            rd(order[q][2]);
-            mfma(c, 4 + q, 4);
-            mfma(c, 4 + q, 5);
-            rd(order[q][3]);
-            mfma(c, 4 + q, 6);
-            mfma(c, 4 + q, 7);
+        for (int r = 0; r < 8; ++r) {
+            if ((r & 1) == 0) dma_part(rc, kdma, r >> 1);
+            mfma(c, r, 0);
+            mfma(c, r, 1);
+            rd(2 * r);
+            mfma(c, r, 2);
+            mfma(c, r, 3);
+            mfma(c, r, 4);
+            rd(2 * r + 1);
+            mfma(c, r, 5);
+            mfma(c, r, 6);
+            mfma(c, r, 7);
         }
         __builtin_amdgcn_sched_barrier(0);
     };
