@@ -12,9 +12,10 @@
 //    workgroup per CU, 1024 tiles at 8192^3 = exactly four rounds of 256 CUs;
 //  * full tiles (the large_mm shape) take gemm_bf16_full_kernel further down:
 //    8 x 8 v_mfma_f32_16x16x32_bf16 per wave and 32-deep k stage, both
-//    operands global -> LDS by DMA into a four-stage ring (no staging
-//    registers, no LDS store instructions), B transposed by the LDS reads
-//    (ds_read_b64_tr_b16);
+//    operands global -> LDS by DMA (no staging registers, no LDS store
+//    instructions) into rings that fill all 160 KB of LDS (A in 64-deep
+//    slots of whole 128-byte lines, B in 32-deep slots), B transposed by the
+//    LDS reads (ds_read_b64_tr_b16);
 //  * other shapes take gemm_bf16_kernel (4 x 4 v_mfma_f32_32x32x16_bf16 per
 //    wave), BK = 64 with an LDS double buffer:
 //    both operands stored K-contiguous, row pitch 72 bf16 (144 B), 2 x 2 x
@@ -221,57 +222,59 @@ void gemm_bf16_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict
 // ---- full-tile kernel (M, N multiples of 256, K of 128, operands < 2 GiB) ----
 // Both operands go global -> LDS by DMA (buffer_load ... lds): no staging
 // registers and no LDS store instructions, whose VGPR reads stall the MFMA
-// issue.  The LDS holds a ring of four 32-deep k stages (A 16 KB + B 16 KB
-// each), so a stage's DMAs are issued three stages before its MFMAs (a
-// two-stage lead, or a five-buffer ring of 160 KB, measured slower):
-//  * A [256 rows][32 k], 64-byte rows; chunk c (8 k) of row r sits in slot
-//    c ^ ((r / 4) % 4).  The 16x16x32 A operand of row block i is one
-//    ds_read_b128: lane l reads row 16 i + l%16, chunk l/16; each 16 lanes
-//    (16 consecutive rows, one chunk) hit 16 distinct 16-byte bank groups;
-//  * B [32 k][256 n] row-major as in HBM, 512-byte rows; chunk c (8 n) of
-//    k-row r sits in slot c ^ f(r), f(r) = 4 (r % 4) ^ 2 ((r / 8) % 2).  The
-//    B operand (8 consecutive k of one column) is two ds_read_b64_tr_b16: in
-//    16-lane group g lane s points at k-row 8 g + 4 q + s/4, columns
-//    n0 + 4 (s % 4) .. +3, and receives column n0 + s, those 4 k-rows.  The
-//    ^ 2 ((r/8) % 2) term puts k-rows r and r + 8 (groups 0 and 1, read in
-//    the same LDS cycle) in different banks;
+// issue.  All 160 KB of LDS hold the operand rings:
+//  * A in three 64-deep slots (32 KB each: 256 rows of 128 bytes).  Each A
+//    DMA instruction fills 8 whole 128-byte lines (8 rows x 8 chunks); chunk c
+//    (8 k) of row r sits in slot c ^ ((r / 2) % 8).  The 16x16x32 A operand of
+//    row block i is one ds_read_b128: lane l reads row 16 i + l%16, chunk
+//    4 h + l/16 (h = which 32-k half of the slot); each 16 lanes hit 16
+//    distinct 16-byte bank groups;
+//  * B in four 32-deep slots (16 KB each: [32 k][256 n] row-major as in HBM,
+//    512-byte k-rows); chunk c (8 n) of k-row r sits in slot c ^ f(r),
+//    f(r) = 4 (r % 4) ^ 2 ((r / 8) % 2).  The B operand (8 consecutive k of one
+//    column) is two ds_read_b64_tr_b16: in 16-lane group g lane s points at
+//    k-row 8 g + 4 q + s/4, columns n0 + 4 (s % 4) .. +3, and receives column
+//    n0 + s, those 4 k-rows.  The ^ 2 ((r/8) % 2) term puts k-rows r and r + 8
+//    (groups 0 and 1, read in the same LDS cycle) in different banks;
 //  * each DMA instruction writes a wave's 64 x 16 B contiguously, so lane l
 //    fetches the global chunk that its slot holds.
 // The MFMA is v_mfma_f32_16x16x32_bf16, not 32x32x16: on random bf16 data
 // the chip is power-limited, and a register-only loop of 16x16x32 sustains
-// 1.90-2.12 PF against 1.50-1.85 PF for 32x32x16 at the same power.  In the
-// GEMM it took an 8192^3 launch from 791-816 us to 756-773 us on the same box
-// (bit-identical output: every k32 sum rounds to the same bf16).
-// Stage s (buffer s % 4, operands in register set s % 2): wait for this
-// wave's DMAs of stage s+1 and pass one LDS barrier (every wave finished
-// reading stage s during stage s-1, and every wave's stage s+1 DMAs have
-// landed); then the wave's 8 x 8 blocks (64 MFMAs) run with the refill of
-// buffer s % 4 (stage s+4) and the reads of all of stage s+1's operands into
-// the other register set spread evenly under them.  With the barrier in the
-// middle of the stage instead (reads and DMAs under the second half only) the
-// LDS queue was oversubscribed in that half: 590 -> 561 us on zero operands,
-// 805-809 -> 794-802 us on random ones (power-limited), same box.
-constexpr int KS = 32;                    // k per LDS stage
-constexpr int AROWB = KS * 2;             // bytes per A row in LDS
+// 1.90-2.12 PF against 1.50-1.85 PF for 32x32x16 at the same power.
+//
+// Stage s (32 k; B slot s % 4, operands in register set s % 2): wait for this
+// wave's DMAs issued three stages earlier and pass one LDS barrier (every
+// wave finished reading the slots refilled below, and stage s+1 has landed);
+// then the wave's 8 x 8 blocks (64 MFMAs) run with one DMA instruction per
+// row of 8 MFMAs (B stage s+4 into slot s % 4 on even rows, a quarter of A
+// pair (s+1)/2 + 2 on odd rows) and the 24 reads of stage s+1's operands
+// spread under them.  Measured on random operands, power-limited (1400 W),
+// same box, 8192^3: 32-deep A and B slots with both DMAs every other row
+// 762-772 us; one DMA per row 758-763 us (on zero operands, not
+// power-limited, 585 -> 521 us: two DMAs at once stall the MFMA issue); A
+// in 128-byte lines as here 735-742 us.  Per 32-k stage the loop takes ~1256
+// cycles for 1024 cycles of MFMA work: ~62 at the barrier, ~8 waiting for
+// DMAs, the rest issue gaps, ~16 cycles per DMA instruction.  A 64-byte A
+// row (the 32-deep A slot) makes each DMA instruction touch 16 half lines
+// instead of 8 whole ones; in cycles both run alike, but the whole-line
+// version spends less energy per GEMM, so at the power limit it keeps a
+// higher clock.
+constexpr int KS = 32;                    // k per B slot and per barrier
 constexpr int BROWB = BN * 2;             // bytes per B k-row in LDS
-constexpr int STAGE_A = BM * KS;          // bf16 per A stage
-constexpr int STAGE_ELEMS = STAGE_A + KS * BN;
+constexpr int A_SLOT_BYTES = BM * 128;    // one A slot: 64 k
+constexpr int B_SLOT_BYTES = KS * BROWB;  // one B slot: 32 k
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
-
-
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(256, 1)
 void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                            uint16_t* __restrict__ C, uint32_t M, uint32_t N, uint32_t K,
                            uint32_t tiles_m, uint32_t tiles_n) {
-    __shared__ __attribute__((aligned(1024))) uint16_t L0[STAGE_ELEMS];
-    __shared__ __attribute__((aligned(1024))) uint16_t L1[STAGE_ELEMS];
-    __shared__ __attribute__((aligned(1024))) uint16_t L2[STAGE_ELEMS];
-    __shared__ __attribute__((aligned(1024))) uint16_t L3[STAGE_ELEMS];
+    __shared__ __attribute__((aligned(1024))) uint8_t AL[3 * A_SLOT_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t BL[4 * B_SLOT_BYTES];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63;
@@ -282,33 +285,39 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(tm * BM);
     const uint32_t n0 = __builtin_amdgcn_readfirstlane(tn * BN);
     const uint32_t nstages = K / KS;   // a multiple of 4
+    const uint32_t npairs = nstages / 2;
     const uint32_t last_k0 = (nstages - 1) * KS;
 
     const i32x4 ars = dma_rsrc(A, M * K * 2), brs = dma_rsrc(B, K * N * 2);
+    const uint32_t al = lds_addr(AL), bl = lds_addr(BL);
 
-    // A DMA: instruction i of wave w fills rows 64 w + 16 i + l/4, slot l%4,
-    // which holds chunk (l%4) ^ ((l/16) % 4).
-    const uint32_t a_voff = ((lane >> 2) * K + 8 * ((lane & 3) ^ ((lane >> 4) & 3))) * 2;
-    // B DMA: instruction i of wave w fills k-rows r = 8 w + 2 i + l/32, slot
-    // l%32, which holds chunk (l%32) ^ f(r), f(r) = 4 (r % 4) ^ 2 ((r / 8) % 2):
-    // k-rows r and r + 8, read by the same half-wave of ds_read_b64_tr_b16,
-    // land in different banks.
+    // A DMA instruction i (0..7) of wave w for pair q (k 64 q .. 64 q + 63):
+    // rows 64 w + 8 i + l/8, slot l%8, which holds chunk
+    // (l%8) ^ ((row/2) % 8) = (l%8) ^ ((4 i + l/16) % 8).
+    uint32_t a_voff[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+        a_voff[p] = ((lane >> 3) * K + 8 * ((lane & 7) ^ ((4 * p + (lane >> 4)) & 7))) * 2;
+    const uint32_t a_dst = 64 * wave * 128;
+    const uint32_t a_src = (m0 + 64 * wave) * K * 2;
+    // B DMA instruction i (0..3) of wave w: k-rows r = 8 w + 2 i + l/32, slot
+    // l%32, which holds chunk (l%32) ^ f(r).
     const uint32_t b_r = lane >> 5;
     const uint32_t bx = 2 * (wave & 1);
     const uint32_t b_voff0 = (b_r * N + 8 * ((lane & 31) ^ (4 * b_r) ^ bx)) * 2;
     const uint32_t b_voff1 = (b_r * N + 8 * ((lane & 31) ^ (4 * (2 + b_r)) ^ bx)) * 2;
-    const uint32_t ring[4] = {(uint32_t)(uintptr_t)(lds_void_t*)L0, (uint32_t)(uintptr_t)(lds_void_t*)L1,
-                              (uint32_t)(uintptr_t)(lds_void_t*)L2, (uint32_t)(uintptr_t)(lds_void_t*)L3};
-    const uint32_t a_dst = 64 * wave * AROWB, b_dst = STAGE_A * 2 + 8 * wave * BROWB;
-    const uint32_t a_src = (m0 + 64 * wave) * K * 2, b_src = (8 * wave * N + n0) * 2;
-    auto dma_part = [&](int rb, uint32_t k0, int i) {
-        dma16(ars, ring[rb] + a_dst + 16 * i * AROWB, a_voff, a_src + (16 * i * K + k0) * 2);
-        dma16(brs, ring[rb] + b_dst + 2 * i * BROWB, (i & 1) ? b_voff1 : b_voff0,
-              b_src + (k0 + 2 * i) * N * 2);
+    const uint32_t b_dst = 8 * wave * BROWB;
+    const uint32_t b_src = (8 * wave * N + n0) * 2;
+    // Pairs past the last one (the ring's tail) reload the last pair into its
+    // own slot: the same bytes, so a concurrent read of it is unaffected.
+    auto dma_a = [&](uint32_t q, int i) {
+        q = min(q, npairs - 1);
+        dma16(ars, al + (q % 3) * A_SLOT_BYTES + a_dst + 8 * i * 128, a_voff[i & 1],
+              a_src + (8 * i * K + 64 * q) * 2);
     };
-    auto dma = [&](int rb, uint32_t k0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dma_part(rb, k0, i);
+    auto dma_b = [&](int slot, uint32_t k0, int i) {
+        dma16(brs, bl + slot * B_SLOT_BYTES + b_dst + 2 * i * BROWB, (i & 1) ? b_voff1 : b_voff0,
+              b_src + (k0 + 2 * i) * N * 2);
     };
 
     f32x4 acc[8][8];
@@ -318,9 +327,10 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
         for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{};
 
     // 16x16x32 operands.  A (i): lane l holds row wm*128 + 16 i + l%16,
-    // k octet l/16 (chunk l/16 of the row, in slot chunk ^ ((row/4) % 4)).
+    // k octet l/16 of the stage's 32-k half h.
     const uint32_t g = lane >> 4, t = lane & 15;
-    const uint32_t a_row = (wm * 128 + t) * AROWB, a_slot = 16 * (g ^ ((t >> 2) & 3));
+    const uint32_t a_row = (wm * 128 + t) * 128;
+    const uint32_t a_half[2] = {16 * ((0 + g) ^ ((t >> 1) & 7)), 16 * ((4 + g) ^ ((t >> 1) & 7))};
     // B (j): lane l needs column wn*128 + 16 j + l%16, k = 8 (l/16) .. +7:
     // two ds_read_b64_tr_b16 (k-rows 8g + 4q + t/4, columns 4 (t%4) .. +3 of
     // the 16-column block), each returning 4 k of column t.
@@ -343,7 +353,7 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
         return __builtin_bit_cast(bf16x8, u32x4{h[0][0], h[0][1], h[1][0], h[1][1]});
     };
     auto a_at = [&](const uint8_t* as, int i) {
-        return *reinterpret_cast<const bf16x8*>(as + 16 * i * AROWB + a_slot);
+        return *reinterpret_cast<const bf16x8*>(as + 16 * i * 128);
     };
     bf16x8 a[2][8], b[2][8];
     // The MFMAs are inline asm with the accumulators pinned to AccVGPRs
@@ -352,31 +362,39 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
     // The wait-count pass sees the asm operands (it waits for the operand
     // reads); the one hazard it cannot see -- reading an accumulator right
     // after the MFMA that writes it -- is padded before the epilogue.
+    // Consecutive MFMAs share an operand register (snake order over j).
     auto mfma = [&](int c, int i, int jj) {
         const int j = (i & 1) ? 7 - jj : jj;
         asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
                      : "+a"(acc[i][j]) : "v"(a[c][i]), "v"(b[c][j]));
     };
-    // Stage s on ring buffer rc, operands in register set c.  Stage s+1's
-    // operands are read two per row of MFMAs in the order they are consumed
-    // (its first row needs every B and A0, the later rows one A each), and
-    // the refill goes out as one DMA part every other row.
-    auto stage = [&](int rc, int c, const uint16_t* nxt, uint32_t kdma) {
+    // Stage s at unrolled position u = s % 4.  A pair q occupies slot q % 3
+    // and is fetched a quarter per stage over stages 2q - 5 and 2q - 4, i.e.
+    // three stages before its first read; its slot held pair q - 3, whose
+    // last operands were read during stage 2q - 6.
+    auto stage = [&](int u, uint32_t s) {
+        const int c = u & 1;
+        const uint32_t qn = (s + 1) >> 1;          // pair holding stage s+1
+        const uint32_t qd = qn + 2;                // pair being fetched
+        const int ih = 4 * ((u + 1) & 1);          // its instructions 0-3 (s odd) or 4-7
+        const uint32_t kb = min((s + 4) * KS, last_k0);
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(0x4F70);   // vmcnt(16): stages s+2, s+3 may be in flight
+        __builtin_amdgcn_s_waitcnt(0x4F70);   // vmcnt(16): stages s-1, s-2 may be in flight
         lds_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        const uint8_t* nas = reinterpret_cast<const uint8_t*>(nxt) + a_row;
-        const uint8_t* nbs = reinterpret_cast<const uint8_t*>(nxt + STAGE_A);
-        // unit u < 8: B u (two transposing reads); u >= 8: A u-8 (one read)
-        auto rd = [&](int u) {
-            if (u < 8) b[c ^ 1][u] = b_at(nbs, u);
-            else a[c ^ 1][u - 8] = a_at(nas, u - 8);
+        const uint8_t* nas = AL + (qn % 3) * A_SLOT_BYTES + a_row + a_half[(u + 1) & 1];
+        const uint8_t* nbs = BL + ((u + 1) & 3) * B_SLOT_BYTES;
+        // unit v < 8: B v (two transposing reads); v >= 8: A v-8 (one read),
+        // in the order stage s+1 consumes them (its first row needs every B)
+        auto rd = [&](int v) {
+            if (v < 8) b[c ^ 1][v] = b_at(nbs, v);
+            else a[c ^ 1][v - 8] = a_at(nas, v - 8);
         };
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
-            if ((r & 1) == 0) dma_part(rc, kdma, r >> 1);
             mfma(c, r, 0);
+            if (r & 1) dma_a(qd, ih + (r >> 1));
+            else dma_b(u, kb, r >> 1);
             mfma(c, r, 1);
             rd(2 * r);
             mfma(c, r, 2);
@@ -390,32 +408,45 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    dma(0, 0);
-    dma(1, KS);
-    dma(2, 2 * KS);
-    dma(3, 3 * KS);
-    __builtin_amdgcn_s_waitcnt(0x4F78);   // vmcnt(24): stage 0 has landed
-    lds_barrier();
-    {
-        const uint8_t* as = reinterpret_cast<const uint8_t*>(L0) + a_row;
-        const uint8_t* bs = reinterpret_cast<const uint8_t*>(L0 + STAGE_A);
+    // Prologue: A pairs 0-2 and B stages 0-3, in the order A0 B0 B1 A1 B2 B3
+    // A2 (40 DMA instructions per wave).  Stage 0's barrier then waits for
+    // the first 24 (A0 B0 B1 A1) and stage 0 reloads the second half of A2.
 #pragma unroll
-        for (int i = 0; i < 8; ++i) { a[0][i] = a_at(as, i); b[0][i] = b_at(bs, i); }
+    for (int i = 0; i < 8; ++i) dma_a(0, i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma_b(0, 0, i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma_b(1, KS, i);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dma_a(1, i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma_b(2, 2 * KS, i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma_b(3, 3 * KS, i);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dma_a(2, i);
+    __builtin_amdgcn_s_waitcnt(0x4F7C);   // vmcnt(28): A pair 0 and B stage 0 have landed
+    lds_barrier();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        a[0][i] = a_at(AL + a_row + a_half[0], i);
+        b[0][i] = b_at(BL, i);
     }
     for (uint32_t s = 0; s < nstages; s += 4) {
-        stage(0, 0, L1, min((s + 4) * KS, last_k0));
-        stage(1, 1, L2, min((s + 5) * KS, last_k0));
-        stage(2, 0, L3, min((s + 6) * KS, last_k0));
-        stage(3, 1, L0, min((s + 7) * KS, last_k0));
+        stage(0, s);
+        stage(1, s + 1);
+        stage(2, s + 2);
+        stage(3, s + 3);
     }
     __builtin_amdgcn_s_waitcnt(0);   // no DMA may still target LDS
     // the last MFMAs' results must be written before they are read
     asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory");
 
-    // Epilogue through LDS: lane l, reg r of 16x16 block (i, j) is row
-    // 16 i + 4 (l/16) + r, column 16 j + l%16 of the wave's 128 x 128 tile.
+    // Epilogue through LDS (32 KB per wave: the three A slots and the first
+    // two B slots): lane l, reg r of 16x16 block (i, j) is row 16 i + 4 (l/16)
+    // + r, column 16 j + l%16 of the wave's 128 x 128 tile.
     lds_barrier();
-    uint16_t* ct = wave == 0 ? L0 : wave == 1 ? L1 : wave == 2 ? L2 : L3;
+    uint16_t* ct = reinterpret_cast<uint16_t*>(wave < 3 ? AL + wave * A_SLOT_BYTES : BL);
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
