@@ -205,8 +205,9 @@ void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt
 //    16 distinct bank groups 8 (r % 2) + slot;
 //  * a DMA instruction writes a wave's 64 x 16 B = eight rows contiguously;
 //    wave w fetches A rows 8 w .. 8 w + 7 and 8 x BI B rows, lane l the chunk
-//    that slot l % 8 of its row holds.  Taps outside the image and k past the
-//    filter use an out-of-range offset, which the DMA lands as zeros;
+//    that slot l % 8 of its row holds.  Taps outside the image use an
+//    out-of-range offset, which the DMA lands as zeros; fetches past the last
+//    stage re-fetch it into a slot that is never read;
 //  * stage s (slot s % NBUF): group 0 reads group 1's operands under its 4
 //    MFMAs; before group 1 the wave waits for its DMAs of stage s+1, passes an
 //    LDS barrier, refills slot s % NBUF with stage s+NBUF and reads stage
@@ -219,8 +220,13 @@ void conv2d_f32_kernel(const float* __restrict__ X, const float* __restrict__ Wt
 // us against 95.2-96.1 us for the register-staged version of this path
 // (conv2d_f32_kernel's layout with buffer loads); 64-pixel tiles (WMS = 2)
 // 91.5-92.5 us; a ring of three or four stages was slower (fewer workgroups
-// per CU).
+// per CU).  The stage's tap used to be decoded from k0 in the loop (two
+// runtime divisions, bounds checks as branches: ~8 scalar and ~4 vector
+// instructions per MFMA, the MFMA pipe 71 % busy); advanced incrementally
+// instead, with the k and channel offsets in the DMA's scalar offset, the
+// same launch went from 74.8 to 64.3 us at the working clock (bit-identical).
 constexpr int NBUF = 2;
+template <uint32_t V> struct SlotC { static constexpr uint32_t v = V; };
 
 // WMS = 32-pixel row groups per tile (tile BMT = 32 WMS pixels x 64 channels,
 // 4 WMS waves).
@@ -261,34 +267,46 @@ void conv2d_f32_dma_kernel(const float* __restrict__ X, const float* __restrict_
     const uint32_t pp = t % sh.p, nn = t / sh.p;
     const int32_t h0 = (int32_t)(pp * sh.stride) - (int32_t)sh.pad;
     const int32_t w0 = (int32_t)(qq * sh.stride) - (int32_t)sh.pad;
-    const uint32_t xbase = nn * sh.h * sh.w * sh.c + 4 * dch;
+    const uint32_t xbase = (nn * sh.h * sh.w * sh.c + 4 * dch) * 4;   // bytes
+    // This lane's byte offset of tap (r, s), or an out-of-range offset (the
+    // DMA lands zeros) when the tap falls outside the image.
+    auto tap_off = [&](uint32_t r, uint32_t s) -> uint32_t {
+        const uint32_t hi = (uint32_t)(h0 + (int32_t)r), wi = (uint32_t)(w0 + (int32_t)s);
+        const bool in = m_ok && hi < sh.h && wi < sh.w;
+        return in ? xbase + (hi * sh.w + wi) * sh.c * 4 : 0x80000000u;
+    };
     // B rows (output channels) of this wave: BI instructions of 8 rows each
-    uint32_t oc[BI], bch[BI];
-    bool o_ok[BI];
+    uint32_t wbase[BI];
 #pragma unroll
     for (int i = 0; i < BI; ++i) {
         const uint32_t brow = 8 * (BI * wave + i) + (lane >> 3);
-        bch[i] = (lane & 7) ^ ((brow >> 1) & 7);
-        oc[i] = n0 + brow;
-        o_ok[i] = oc[i] < sh.o;
+        const uint32_t bch = (lane & 7) ^ ((brow >> 1) & 7);
+        const uint32_t oc = n0 + brow;
+        wbase[i] = oc < sh.o ? (oc * sh.k + 4 * bch) * 4 : 0x80000000u;
     }
     const uint32_t l0 = lds_addr(L);
     const uint32_t dst = 8 * wave * 128;   // this wave's A rows in a slot
-    auto dma = [&](uint32_t slot, uint32_t k0) {
-        // uniform tap of the stage: k0 = (r*S + s)*C + c0 (k0 past the filter
-        // reads as an image miss)
-        const uint32_t rs = k0 / sh.c, c0 = k0 - rs * sh.c;
-        const uint32_t r = rs / sh.s, s = rs - r * sh.s;
-        const int32_t hi = h0 + (int32_t)r, wi = w0 + (int32_t)s;
-        const bool in = m_ok && k0 < sh.k && hi >= 0 && hi < (int32_t)sh.h && wi >= 0 &&
-                        wi < (int32_t)sh.w;
-        const uint32_t xo = in ? (xbase + ((uint32_t)hi * sh.w + wi) * sh.c + c0) * 4 : 0x80000000u;
-        dma16(xrs, l0 + slot * (C_SLOT * 4) + dst, xo, 0);
+    // The next stage to fetch: k offset kd, tap (tr, ts), channel offset tc.
+    // Advanced incrementally (no division in the loop); the k and channel
+    // offsets ride in the DMA's scalar offset, so only a tap change touches
+    // the per-lane offset.  Fetches past the last stage re-fetch it into a
+    // slot that is never read (the same bytes, in bounds).
+    uint32_t kd = 0, tr = 0, ts = 0, tc = 0;
+    uint32_t xoff = tap_off(0, 0);
+    auto dma_next = [&](uint32_t slot) {
+        dma16(xrs, l0 + slot * (C_SLOT * 4) + dst, xoff, tc * 4);
 #pragma unroll
-        for (int i = 0; i < BI; ++i) {
-            const uint32_t wo =
-                (o_ok[i] && k0 < sh.k) ? (oc[i] * sh.k + k0 + 4 * bch[i]) * 4 : 0x80000000u;
-            dma16(wrs, l0 + slot * (C_SLOT * 4) + A_BYTES + 8 * (BI * wave + i) * 128, wo, 0);
+        for (int i = 0; i < BI; ++i)
+            dma16(wrs, l0 + slot * (C_SLOT * 4) + A_BYTES + 8 * (BI * wave + i) * 128, wbase[i],
+                  kd * 4);
+        if (kd + BK < sh.k) {
+            kd += BK;
+            tc += BK;
+            if (tc == sh.c) {
+                tc = 0;
+                if (++ts == sh.s) { ts = 0; ++tr; }
+                xoff = tap_off(tr, ts);
+            }
         }
     };
 
@@ -312,28 +330,34 @@ void conv2d_f32_dma_kernel(const float* __restrict__ X, const float* __restrict_
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[c].z, b4[c].z, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[c].w, b4[c].w, acc, 0, 0, 0);
     };
-
-#pragma unroll
-    for (uint32_t st = 0; st < NBUF; ++st) dma(st, st * BK);
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (D * (NBUF - 1)));   // stage 0 has landed
-    lds_barrier();
-    read_ops(0, 0, 0);
-    // DMAs past the last stage land as zeros in slots that are never read.
-    uint32_t slot = 0;
-    for (uint32_t st = 0; st < nstages; ++st) {
-        const uint32_t nslot = slot + 1 == NBUF ? 0 : slot + 1;
+    // Stage s in slot s % 2: group 0 reads group 1's operands under its 4
+    // MFMAs; the wave waits for its DMAs of stage s+1, passes an LDS barrier,
+    // refills slot s % 2 with stage s+2 and reads stage s+1's first operands
+    // under group 1's MFMAs.
+    auto stage = [&](auto SL) {
+        constexpr uint32_t slot = decltype(SL)::v, nslot = slot ^ 1u;
         __builtin_amdgcn_sched_barrier(0);
         read_ops(slot, 1, 1);
         mfma4(0);
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (D * (NBUF - 2)));   // stage st+1 has landed
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): stage s+1 has landed
         lds_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        dma(slot, (st + NBUF) * BK);
+        dma_next(slot);
         read_ops(nslot, 0, 0);
         mfma4(1);
         __builtin_amdgcn_sched_barrier(0);
-        slot = nslot;
+    };
+
+    static_assert(NBUF == 2, "the loop below alternates two slots");
+    dma_next(0);
+    dma_next(1);
+    __builtin_amdgcn_s_waitcnt(0x0F70 | D);   // vmcnt(D): stage 0 has landed
+    lds_barrier();
+    read_ops(0, 0, 0);
+    for (uint32_t st = 0; st < nstages; st += 2) {
+        stage(SlotC<0>{});
+        if (st + 1 < nstages) stage(SlotC<1>{});
     }
     __builtin_amdgcn_s_waitcnt(0);   // no DMA may still target LDS
     lds_barrier();
