@@ -24,6 +24,10 @@ multi-kernel step): `roofline.achieved` is the algorithmic bytes (HBM-bound
 kernels) or flops (MFMA-bound kernels) of ONE launch of the dominant kernel
 divided by that kernel's mean event-timed duration over those K steps.
 
+HBM-bound records also carry `measured_peak` / `frac_of_measured`: the same
+achieved rate against what the library's copy kernel moves on this box, cold
+(`hbm_measured_gbps`, measured at start-up), beside the datasheet fraction.
+
 cpu_baseline: the registry's torch-CPU Model spec (the harness's `mlx ref`
 line) timed on all host cores over the full workload -- a reported baseline,
 not a target.
@@ -112,6 +116,10 @@ def _roofline(name: str, w: dict, k_t: dict, compute_dtype: str) -> dict:
     out = {"bound": w["bound"], "achieved": achieved, "peak": peak, "unit": unit,
            "frac": achieved / peak, "traffic": _traffic(kernel or name),
            "kernel_mean_us": mean_ms * 1e3}
+    if w["bound"] == "hbm" and "gbps" in _MEASURED_HBM:
+        # against what a plain copy kernel moves on this box, cold
+        out["measured_peak"] = _MEASURED_HBM["gbps"]
+        out["frac_of_measured"] = achieved / _MEASURED_HBM["gbps"]
     if kernel or w.get("label"):
         out["kernel"] = kernel or w["label"]
     return out
@@ -159,6 +167,49 @@ def _cpu_baseline(name: str, b, inputs, meta: dict) -> dict:
                       f"(torch {torch.__version__}, {torch.get_num_threads()} threads on "
                       f"{H.cpu_model()}, {platform.machine()}); median of {iters} after 1 "
                       f"warmup, {t['median_ms']:.1f} ms per step"}
+
+
+_MEASURED_HBM = {}
+
+
+def _measured_hbm_gbps() -> float:
+    """Achievable HBM bandwidth of this box: the library's copy kernel over
+    512 MiB (read) + 512 MiB (write), rotated over two buffer pairs so no
+    launch finds its bytes in the 256 MB memory-side cache, after the same
+    clock settle as the workloads; device time of 20 back-to-back launches.
+    Measured once per process."""
+    if "gbps" in _MEASURED_HBM:
+        return _MEASURED_HBM["gbps"]
+    import ctypes
+
+    import torch
+
+    from metalbench_amd import native
+
+    lib = native.load()
+    n = (512 << 20) // 4
+    pairs = [(torch.empty(n, device="cuda"), torch.empty(n, device="cuda")) for _ in range(2)]
+    for src, _ in pairs:
+        src.fill_(1.0)
+    stream = torch.cuda.Stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+
+    def launch_n(count):
+        for i in range(count):
+            src, dst = pairs[i % 2]
+            native.check("mb_launch_copy_f32", lib.mb_launch_copy_f32(src.data_ptr(), dst.data_ptr(),
+                                                                       n, sp))
+    with torch.cuda.stream(stream):
+        _settle(launch_n, 30.0)
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(stream)
+        launch_n(20)
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    sec = ev0.elapsed_time(ev1) / 20 * 1e-3
+    _MEASURED_HBM["gbps"] = 2 * n * 4 / sec / 1e9
+    del pairs
+    return _MEASURED_HBM["gbps"]
 
 
 def _copy_calibration(n_bytes: int = 256 << 20, launches: int = 3) -> None:
@@ -394,6 +445,7 @@ def main(argv=None):
     names = native.kernel_names()
     if args.copy_calibration:
         _copy_calibration()
+    _measured_hbm_gbps()
 
     others = [n for n in ("transpose_2d", "sqr_mm", "conv2d", "large_mm") if n != args.workload]
     if args.only:
@@ -439,6 +491,7 @@ def main(argv=None):
         "cache": head["cache"],
         "clock_settle_ms": head["clock_settle_ms"],
         "cpu_baseline": head.get("cpu_baseline"),
+        "hbm_measured_gbps": _MEASURED_HBM.get("gbps"),
         "gpu_mean_ms": head["gpu_mean_ms"],
         "parts": head.get("parts"),
         "kernels": kernels,

@@ -89,3 +89,15 @@ def test_cold_start_timing_evicts_and_keeps_results(mb):
     with pytest.raises(native.NativeError) as e:
         native.run(kid, binds, 0, 2, native.RUN_COLD | native.RUN_WALL_ONLY)
     assert e.value.code == -7
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 1023, 4096, 4096 * 257 + 5])
+def test_copy_bit_exact(mb, dev, n):
+    """The copy kernel (the HBM-ceiling and counter-calibration kernel that
+    bench.py runs): bit-exact for any length, the tail past the last whole
+    16-byte vector included."""
+    a = seeded(n, (n,))
+    d_a = a.to(dev)
+    d_b = torch.full((n,), float("nan"), device=dev)
+    launch("mb_launch_copy_f32", ptr(d_a), ptr(d_b), n, None)
+    assert np.array_equal(bits32(d_b), a.numpy().view(np.int32))
