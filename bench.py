@@ -433,8 +433,8 @@ def main(argv=None):
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only (every config fits one MI355X; "
-              "the multi-GPU sharding is described in DESIGN.md, not run). Use --gpus 1.",
+        print("bench.py: this build measures one GPU only (every config fits one MI355X, and "
+              "the multi-GPU sharding of the decode step is a design, not a run). Use --gpus 1.",
               file=sys.stderr)
         return 2
 
