@@ -48,31 +48,45 @@ METRIC = "TFLOP/s or GB/s as % of MI355X roofline per kernel; decoder block µs/
 HBM_PEAK_GBPS = 8000.0
 MFMA_PEAK_TFLOPS = {"f32": 157.3, "bf16": 2516.6}
 
-# Decoder decode-step shapes (registry mlx/kernels/full/registry.py).
-_B, _D, _H, _HKV, _DH, _FF, _L = 16, 4096, 32, 8, 128, 14336, 2048
+# Decode-step workloads (registry mlx/kernels/full/registry.py): the whole
+# layer and one GPU's share of it under 8-way tensor parallelism.
+DECODE_STEPS = ("llama_decoder_step", "llama_decoder_step_tp8")
 
 
-def _decoder_part_bytes() -> dict:
+def _step_shape(meta: dict) -> dict:
+    """B, D, H, Hkv, Dh, FF, L of a decode-step registry entry, from its scalars."""
+    sc = {s["binding"]: s["value"] for s in meta["scalars"]}
+    return dict(B=sc[10], D=sc[11], H=sc[12], HKV=sc[13], DH=128, FF=sc[14], L=sc[15])
+
+
+def _decoder_part_bytes(meta: dict | None = None) -> dict:
     """Algorithmic HBM bytes of one launch of each decoder kernel: every weight
-    and cache byte once, activations in and out once (bf16 = 2 bytes)."""
-    qkv_n = _D + 2 * _HKV * _DH
+    and cache byte once, activations in and out once (bf16 = 2 bytes).  The
+    attention width QD = H * Dh is D for a whole layer."""
+    if meta is None:
+        from metalbench_amd import helpers as H
+        meta = H.load_baseline("llama_decoder_step").meta
+    t = _step_shape(meta)
+    B, D, HKV, DH, FF, L = t["B"], t["D"], t["HKV"], t["DH"], t["FF"], t["L"]
+    QD = t["H"] * DH
+    qkv_n = QD + 2 * HKV * DH
     return {
-        "qkv_rope": 2 * (_D * qkv_n + _B * _D + _B * _D + 2 * _B * _HKV * _DH),
-        "attention": 2 * (2 * _B * _HKV * _L * _DH + _B * _D),
-        "wo_residual": 2 * (_D * _D + 2 * _B * _D) + 4 * _B * _D,
-        "gate_up_swiglu": 2 * (_D * 2 * _FF + _B * _D + _B * _FF),
-        "down_residual": 2 * (_FF * _D + _B * _FF + _B * _D) + 4 * _B * _D,
+        "qkv_rope": 2 * (D * qkv_n + B * D + B * QD + 2 * B * HKV * DH),
+        "attention": 2 * (2 * B * HKV * L * DH + B * QD),
+        "wo_residual": 2 * (QD * D + B * QD + B * D) + 4 * B * D,
+        "gate_up_swiglu": 2 * (D * 2 * FF + B * D + B * FF),
+        "down_residual": 2 * (FF * D + B * FF + B * D) + 4 * B * D,
     }
 
 
 # Per workload: (dominant part name or None for single-kernel, bound, units of
 # algorithmic work per launch, unit of `value`).
 def _work(name: str, meta: dict):
-    if name == "llama_decoder_step":
+    if name in DECODE_STEPS:
         # The roofline is priced on the whole step (its five kernels and the
         # dispatch gaps between them) over the back-to-back timed region; the
         # per-kernel figures stay in `parts`.
-        parts = _decoder_part_bytes()
+        parts = _decoder_part_bytes(meta)
         return dict(part=None, bound="hbm", per_launch=sum(parts.values()), parts=parts,
                     label="decode step: qkv_rope, attention, wo_residual, gate_up_swiglu, "
                           "down_residual")
@@ -90,7 +104,7 @@ def _bound(meta: dict) -> str:
 
 
 def _value_unit(name: str, meta: dict, ms_per_step: float):
-    if name == "llama_decoder_step":
+    if name in DECODE_STEPS:
         return ms_per_step * 1000.0, "us/step", False
     if _bound(meta) == "hbm":
         return meta["bytes"] / (ms_per_step * 1e-3) / 1e9, "GB/s", True
@@ -237,7 +251,9 @@ def _copy_calibration(n_bytes: int = 256 << 20, launches: int = 3) -> None:
 # or the matrix being transposed) is rotated over R device copies, so no step
 # finds the previous step's bytes in the 256 MB memory-side cache (MALL) -- as
 # in a real decode, where every layer streams its own weights and cache.
-ROTATE = {"llama_decoder_step": 3, "transpose_2d": 2}
+# The tensor-parallel shard's working set is ~72 MB, so it takes 6 copies
+# (5 x 72 MB touched between two uses of one copy > 256 MB).
+ROTATE = {"llama_decoder_step": 3, "llama_decoder_step_tp8": 6, "transpose_2d": 2}
 
 
 def _async_launcher(name, b, copies_in, copies_out):
@@ -249,7 +265,7 @@ def _async_launcher(name, b, copies_in, copies_out):
 
     lib = native.load()
     sc = {s.binding: s.value for s in b.scalars()}
-    if name == "llama_decoder_step":
+    if name in DECODE_STEPS:
         args = []
         for ci, co in zip(copies_in, copies_out):
             a = native.MbDecoderStepArgs()
@@ -466,10 +482,14 @@ def main(argv=None):
 
     from metalbench_amd import helpers as H
     meta = H.load_baseline(args.workload).meta
-    if args.workload == "llama_decoder_step":
-        config = {"workload": args.workload, "batch": _B, "kv_len": _L, "d_model": _D,
-                  "n_heads": _H, "n_kv_heads": _HKV, "head_dim": _DH, "d_ff": _FF,
-                  "rope_theta": 500000.0, "parallelism": "single-gpu"}
+    if args.workload in DECODE_STEPS:
+        t = _step_shape(meta)
+        config = {"workload": args.workload, "batch": t["B"], "kv_len": t["L"], "d_model": t["D"],
+                  "n_heads": t["H"], "n_kv_heads": t["HKV"], "head_dim": t["DH"],
+                  "d_ff": t["FF"], "rope_theta": 500000.0,
+                  "parallelism": ("single-gpu" if args.workload == "llama_decoder_step" else
+                                  "one GPU's share of 8-way tensor parallelism, all-reduces "
+                                  "excluded")}
     else:
         config = {"workload": args.workload, "input_shapes": meta["input_shapes"],
                   "parallelism": "single-gpu"}

@@ -223,16 +223,22 @@ int mb_launch_conv2d_nhwc_f32(const float* x, const float* w, float* y,
  * token per sequence that attends to `cache_len` cached positions plus itself:
  *   - the new token's position is cache_len; RoPE angle = pos * base^(-2i/Dh);
  *   - the cache holds keys that already carry their RoPE rotation;
- *   - weights are x @ W layouts: w_qkv [D][D + 2*Hkv*Dh] with columns
+ *   - weights are x @ W layouts: w_qkv [D][QD + 2*Hkv*Dh] with columns
  *     [Q | K | V], w_gu [D][2*FF] with columns [gate | up] (reference
- *     llama_decoder_layer.py:30-32, 43-44).
+ *     llama_decoder_layer.py:30-32, 43-44), QD = H * Dh.
+ * For a whole layer QD = D.  QD < D is one tensor-parallel shard of a layer:
+ * its H of the query heads and Hkv of the kv heads (w_qkv's columns), its
+ * QD rows of W_o and its FF columns of gate and up (FF rows of W_down); the
+ * step then computes that shard's work with the two all-reduces (after W_o
+ * and after W_down) left to the caller, i.e. y = x1 + act @ W_down with
+ * x1 = x + attn @ W_o on the shard's partial products.
  * All tensors are row-major bf16 bit patterns.  The caches are read only; the
  * new token's RoPE'd key and its value are written to k_new / v_new so the
  * caller can append them. */
 typedef struct mb_decoder_step_args {
     uint32_t batch;          /* B   sequences in the step          (16)    */
-    uint32_t d_model;        /* D                                 (4096)  */
-    uint32_t n_heads;        /* H                                  (32)   */
+    uint32_t d_model;        /* D   residual width, a multiple of 128 (4096) */
+    uint32_t n_heads;        /* H   query heads, H * Dh <= 16384   (32)   */
     uint32_t n_kv_heads;     /* Hkv                                (8)    */
     uint32_t head_dim;       /* Dh  (must be 128)                          */
     uint32_t d_ff;           /* FF                                (14336) */
@@ -241,8 +247,8 @@ typedef struct mb_decoder_step_args {
     float    rope_base;      /* 500000                                      */
     float    eps;            /* 1e-5                                        */
     const uint16_t* x;       /* [B][D]                                     */
-    const uint16_t* w_qkv;   /* [D][D + 2*Hkv*Dh]                          */
-    const uint16_t* w_o;     /* [D][D]                                     */
+    const uint16_t* w_qkv;   /* [D][QD + 2*Hkv*Dh]                         */
+    const uint16_t* w_o;     /* [QD][D]                                    */
     const uint16_t* w_gu;    /* [D][2*FF]                                  */
     const uint16_t* w_down;  /* [FF][D]                                    */
     const uint16_t* k_cache; /* [B][Hkv][cache_stride][Dh]                 */

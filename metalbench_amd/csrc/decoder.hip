@@ -146,7 +146,7 @@ __device__ __forceinline__ void reset_counter(uint32_t* counter) {
 }
 
 struct StepParams {
-    uint32_t batch, d, hq, hkv, g, ff, cache_len, cache_stride, nsplit, split_keys;
+    uint32_t batch, d, qd, hq, hkv, g, ff, cache_len, cache_stride, nsplit, split_keys;
     float rope_base, eps;
     const uint16_t *x, *k_cache, *v_cache;
     uint16_t *y, *k_new, *v_new;
@@ -154,11 +154,11 @@ struct StepParams {
     float* partial;            // split-K partials [tiles * splits][16][tile columns]
     uint32_t partial_bytes;
     float* sumsq;              // [qkv tiles * splits][16] sum of x^2 over each split
-    uint16_t* q;               // [B][D] rotated queries * 1/sqrt(Dh), bf16 (MFMA operand)
+    uint16_t* q;               // [B][QD] rotated queries * 1/sqrt(Dh), bf16 (MFMA operand)
     float* attn_part;          // [B][Hkv][nsplit][G][DH + 4]  (o[DH], m, l, pad)
     uint32_t attn_part_bytes;
     uint32_t sumsq_bytes;
-    uint16_t* attn_out;        // [B][D]
+    uint16_t* attn_out;        // [B][QD]  (QD = Hq * Dh, the attention width)
     float* x1;                 // [B][D]
     uint16_t* x1b;             // [B][D]  bf16(x1)
     uint16_t* x1b_lo;          // [B][D]  bf16(x1 - bf16(x1))
@@ -483,17 +483,17 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
             const float r1 = rsqrtf(red_ss[b] / (float)p.d + p.eps);
             const float2 vv = *reinterpret_cast<const float2*>(&red[b * TBN + 2 * i]);
             const float v0 = vv.x * r1, v1 = vv.y * r1;
-            if (base < p.d) {
+            if (base < p.qd) {
                 // pre-scaled by 1/sqrt(Dh) and rounded once for the q.k^T MFMA
                 const float qs = rsqrtf((float)DH);
-                *reinterpret_cast<uint32_t*>(p.q + (size_t)b * p.d + base + 2 * i) =
+                *reinterpret_cast<uint32_t*>(p.q + (size_t)b * p.qd + base + 2 * i) =
                     pack_bf16((v0 * cs - v1 * sn) * qs, (v0 * sn + v1 * cs) * qs);
-            } else if (base < p.d + p.hkv * DH) {
-                const uint32_t kvh = (base - p.d) / DH;
+            } else if (base < p.qd + p.hkv * DH) {
+                const uint32_t kvh = (base - p.qd) / DH;
                 *reinterpret_cast<uint32_t*>(p.k_new + ((size_t)b * p.hkv + kvh) * DH + 2 * i) =
                     pack_bf16(v0 * cs - v1 * sn, v0 * sn + v1 * cs);
             } else {
-                const uint32_t kvh = (base - p.d - p.hkv * DH) / DH;
+                const uint32_t kvh = (base - p.qd - p.hkv * DH) / DH;
                 *reinterpret_cast<uint32_t*>(p.v_new + ((size_t)b * p.hkv + kvh) * DH + 2 * i) =
                     pack_bf16(v0, v1);
             }
@@ -662,7 +662,7 @@ void attention_kernel(StepParams p) {
     static_assert(16 * (DH / 8) == 256, "one 16-byte q chunk per thread");
     const uint32_t qh = tid / (DH / 8), qc = tid % (DH / 8);
     const u32x4 qv = *reinterpret_cast<const u32x4*>(
-        p.q + (size_t)b * p.d + (kvh * G + (qh < G ? qh : 0)) * DH + 8 * qc);
+        p.q + (size_t)b * p.qd + (kvh * G + (qh < G ? qh : 0)) * DH + 8 * qc);
     KVBlock kv[AR];
 #pragma unroll
     for (int u = 0; u < AR - 1; ++u) {
@@ -809,7 +809,7 @@ void attention_kernel(StepParams p) {
 #pragma unroll
         for (int i = 0; i < GT / 4; ++i)
             qa[i] = *reinterpret_cast<const uint32_t*>(
-                p.q + (size_t)b * p.d + (kvh * G + min(wave + 4 * i, G - 1)) * DH + 2 * lane);
+                p.q + (size_t)b * p.qd + (kvh * G + min(wave + 4 * i, G - 1)) * DH + 2 * lane);
 #pragma unroll
         for (int i = 0; i < GT / 4; ++i) {
             float d = __uint_as_float(qa[i] << 16) * __uint_as_float(ka << 16) +
@@ -852,7 +852,7 @@ void attention_kernel(StepParams p) {
         uint2 out;
         out.x = pack_bf16(res[0], res[1]);
         out.y = pack_bf16(res[2], res[3]);
-        *reinterpret_cast<uint2*>(p.attn_out + (size_t)b * p.d + (kvh * G + h) * DH + 4 * d4) = out;
+        *reinterpret_cast<uint2*>(p.attn_out + (size_t)b * p.qd + (kvh * G + h) * DH + 4 * d4) = out;
     }
     reset_counter(&p.attn_counters[bk]);
 }
@@ -907,8 +907,15 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
                     a->n_heads, a->n_kv_heads);
     if (a->n_heads / a->n_kv_heads > MAXG)
         return fail(MB_E_ARG, "decoder step: more than %d query heads per kv head", MAXG);
-    if ((uint64_t)a->n_heads * DH != a->d_model)
-        return fail(MB_E_ARG, "decoder step: d_model %u != n_heads * head_dim", a->d_model);
+    // The attention width n_heads * head_dim is d_model for a whole layer and
+    // smaller for one tensor-parallel shard (its share of the heads; W_o then
+    // has n_heads * head_dim rows).
+    if ((uint64_t)a->n_heads * DH > 16384)
+        return fail(MB_E_ARG, "decoder step: n_heads * head_dim = %llu > 16384",
+                    (unsigned long long)a->n_heads * DH);
+    if (a->d_model == 0 || a->d_model % BN)
+        return fail(MB_E_ARG, "decoder step: d_model %u must be a positive multiple of %d",
+                    a->d_model, BN);
     if (a->d_model > 16384)   // the RMSNorm scale reads at most 8 x 16 column-tile sums per row
         return fail(MB_E_ARG, "decoder step: d_model %u > 16384", a->d_model);
     if (a->d_ff == 0 || a->d_ff % KS)
@@ -919,8 +926,8 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
                     a->cache_len);
     if (!(a->rope_base > 0.f) || !(a->eps >= 0.f))
         return fail(MB_E_ARG, "decoder step: rope_base must be > 0 and eps >= 0");
-    const uint32_t D = a->d_model, FF = a->d_ff, B = a->batch;
-    pl->nqkv = D + 2 * a->n_kv_heads * DH;
+    const uint32_t D = a->d_model, FF = a->d_ff, B = a->batch, QD = a->n_heads * DH;
+    pl->nqkv = QD + 2 * a->n_kv_heads * DH;
     pl->g = a->n_heads / a->n_kv_heads;
     {   // attention: about one workgroup per CU (fewer, longer streams read HBM
         // faster than several per CU); splits of a multiple of AR x 64 keys
@@ -944,7 +951,7 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
     pl->tiles[EPI_DOWN] = D / BN;
     const uint32_t ldw[4] = {pl->nqkv, D, 2 * FF, D};
     for (int i = 0; i < 4; ++i) {
-        const uint32_t k = i == EPI_DOWN ? FF : D;
+        const uint32_t k = i == EPI_DOWN ? FF : i == EPI_WO ? QD : D;
         choose_split(pl->tiles[i], k, pl->ww[i], &pl->splits[i], &pl->kc[i], &pl->ring[i]);
         // the ring's clipped loads run up to RING units past the split
         const uint64_t unit = KS / pl->ww[i];
@@ -967,10 +974,10 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
     pl->off_counters = o; o = align256(o + (size_t)n_counters * 4);
     pl->off_partial = o; o = align256(o + max_part * MROWS * BN * 4);
     pl->off_sumsq = o; o = align256(o + (size_t)pl->tiles[EPI_QKV] * pl->splits[EPI_QKV] * MROWS * 4);
-    pl->off_q = o; o = align256(o + (size_t)B * D * 2);
+    pl->off_q = o; o = align256(o + (size_t)B * QD * 2);
     pl->off_attn_part = o;
     o = align256(o + (size_t)B * a->n_kv_heads * pl->nsplit * pl->g * APITCH * 4);
-    pl->off_attn_out = o; o = align256(o + (size_t)B * D * 2);
+    pl->off_attn_out = o; o = align256(o + (size_t)B * QD * 2);
     pl->off_x1 = o; o = align256(o + (size_t)B * D * 4);
     pl->off_x1b = o; o = align256(o + (size_t)B * D * 2);
     pl->off_x1b_lo = o; o = align256(o + (size_t)B * D * 2);
@@ -1030,7 +1037,8 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
     }
 
     StepParams p;
-    p.batch = a->batch; p.d = a->d_model; p.hq = a->n_heads; p.hkv = a->n_kv_heads; p.g = pl.g;
+    p.batch = a->batch; p.d = a->d_model; p.qd = a->n_heads * DH;
+    p.hq = a->n_heads; p.hkv = a->n_kv_heads; p.g = pl.g;
     p.ff = a->d_ff; p.cache_len = a->cache_len; p.cache_stride = a->cache_stride;
     p.nsplit = pl.nsplit; p.split_keys = pl.split_keys; p.rope_base = a->rope_base; p.eps = a->eps;
     p.x = a->x; p.k_cache = a->k_cache; p.v_cache = a->v_cache;
@@ -1052,7 +1060,7 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
     p.act = reinterpret_cast<uint16_t*>(ws + pl.off_act);
     p.act_lo = reinterpret_cast<uint16_t*>(ws + pl.off_act_lo);
 
-    const uint32_t D = a->d_model, FF = a->d_ff;
+    const uint32_t D = a->d_model, FF = a->d_ff, QD = a->n_heads * DH;
     auto gemm = [&](int epi, const uint16_t* act, const uint16_t* act_lo, uint32_t lda,
                     const uint16_t* w, uint32_t ldw, uint32_t k, uint32_t counter_base) -> GemmCfg {
         GemmCfg g;
@@ -1065,7 +1073,7 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
     const GemmCfg g_qkv =
         gemm(EPI_QKV, a->x, nullptr, D, a->w_qkv, pl.nqkv, D, pl.counter_base[0]);
     const GemmCfg g_wo =
-        gemm(EPI_WO, p.attn_out, nullptr, D, a->w_o, D, D, pl.counter_base[2]);
+        gemm(EPI_WO, p.attn_out, nullptr, QD, a->w_o, D, QD, pl.counter_base[2]);
     const GemmCfg g_gu =
         gemm(EPI_GU, p.x1b, p.x1b_lo, D, a->w_gu, 2 * FF, D, pl.counter_base[3]);
     const GemmCfg g_dn =
@@ -1117,7 +1125,7 @@ int run_decoder(const Bindings& bs, hipStream_t s, PartMarks* pm) {
     void* ptr[10];
     if ((rc = bs.buffer(0, MB_DTYPE_BF16, (uint64_t)B * D * 2, false, &ptr[0], "x")) ||
         (rc = bs.buffer(1, MB_DTYPE_BF16, (uint64_t)D * nqkv * 2, false, &ptr[1], "W_qkv")) ||
-        (rc = bs.buffer(2, MB_DTYPE_BF16, (uint64_t)D * D * 2, false, &ptr[2], "W_o")) ||
+        (rc = bs.buffer(2, MB_DTYPE_BF16, (uint64_t)H * DH * D * 2, false, &ptr[2], "W_o")) ||
         (rc = bs.buffer(3, MB_DTYPE_BF16, (uint64_t)D * 2 * FF * 2, false, &ptr[3], "W_gu")) ||
         (rc = bs.buffer(4, MB_DTYPE_BF16, (uint64_t)FF * D * 2, false, &ptr[4], "W_down")) ||
         (rc = bs.buffer(5, MB_DTYPE_BF16, kv * 2, false, &ptr[5], "K_cache")) ||

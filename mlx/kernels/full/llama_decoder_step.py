@@ -17,10 +17,11 @@ import torch.nn.functional as F
 class Model(torch.nn.Module):
     """One decode step of a LLaMA decoder layer.
 
-    Inputs:
+    Inputs (QD = H * D_head; QD = D for a whole layer, QD < D for one
+    tensor-parallel shard computed alone, without the all-reduces):
         x        (B, D)
-        W_qkv    (D, D + 2*H_kv*D_head)   columns [Q | K | V]
-        W_o      (D, D)
+        W_qkv    (D, QD + 2*H_kv*D_head)  columns [Q | K | V]
+        W_o      (QD, D)
         W_gu     (D, 2*FF)                columns [gate | up]
         W_down   (FF, D)
         K_cache  (B, H_kv, L, D_head)     rotated keys of positions 0..L-1
@@ -28,23 +29,25 @@ class Model(torch.nn.Module):
     Outputs: y (B, D), k_new (B, H_kv, D_head), v_new (B, H_kv, D_head)
     """
 
-    def __init__(self, B=16, D=4096, H=32, H_kv=8, FF=14336, L=2048, base=500000.0, eps=1e-5):
+    def __init__(self, B=16, D=4096, H=32, H_kv=8, FF=14336, L=2048, base=500000.0, eps=1e-5,
+                 D_head=None):
         super().__init__()
         self.B, self.D, self.H, self.H_kv, self.FF, self.L = B, D, H, H_kv, FF, L
         self.base, self.eps = base, eps
-        self.D_head = D // H
+        self.D_head = D // H if D_head is None else D_head
+        self.QD = H * self.D_head
         self.G = H // H_kv
 
     def forward(self, x, W_qkv, W_o, W_gu, W_down, K_cache, V_cache):
-        B, D, H, H_kv, Dh, FF, G = self.B, self.D, self.H, self.H_kv, self.D_head, self.FF, self.G
+        B, QD, H, H_kv, Dh, FF, G = self.B, self.QD, self.H, self.H_kv, self.D_head, self.FF, self.G
         x = x.float()
 
         # ---- attention ----
         h = self._rms_norm(x)
         qkv = h @ W_qkv.float()
-        q = qkv[:, :D].reshape(B, H, Dh)
-        k = qkv[:, D:D + H_kv * Dh].reshape(B, H_kv, Dh)
-        v = qkv[:, D + H_kv * Dh:].reshape(B, H_kv, Dh)
+        q = qkv[:, :QD].reshape(B, H, Dh)
+        k = qkv[:, QD:QD + H_kv * Dh].reshape(B, H_kv, Dh)
+        v = qkv[:, QD + H_kv * Dh:].reshape(B, H_kv, Dh)
         q = self._rope(q, self.L)
         k = self._rope(k, self.L)
         keys = torch.cat([K_cache.float(), k[:, :, None, :]], dim=2)     # (B, H_kv, L+1, Dh)
@@ -52,7 +55,7 @@ class Model(torch.nn.Module):
         qg = q.reshape(B, H_kv, G, Dh)                                   # head h -> kv head h // G
         scores = (qg @ keys.transpose(2, 3)) / math.sqrt(Dh)             # (B, H_kv, G, L+1)
         attn = torch.softmax(scores, dim=-1)
-        out = (attn @ vals).reshape(B, D) @ W_o.float()
+        out = (attn @ vals).reshape(B, QD) @ W_o.float()
         x = x + out
 
         # ---- SwiGLU FFN ----

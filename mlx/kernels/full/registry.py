@@ -17,40 +17,53 @@ REGISTRY = {}
 # position 2048 attends to all 2049.  Weights normal(0, 0.02), x and caches
 # normal(0, 1), all bf16.  Outputs: y [B, D], and the new token's rotated key
 # and value [B, Hkv, Dh] for the caller to append.
-_B, _D, _H, _HKV, _DH, _FF, _L = 16, 4096, 32, 8, 128, 14336, 2048
-_QKV = _D + 2 * _HKV * _DH
-_W = _D * _QKV + _D * _D + _D * 2 * _FF + _FF * _D
-REGISTRY["llama_decoder_step"] = dict(
-    metal_function="llama_decoder_step_bf16",
-    threadgroup=(256, 1, 1),
-    input_bindings=(0, 1, 2, 3, 4, 5, 6),
-    input_shapes=[(_B, _D), (_D, _QKV), (_D, _D), (_D, 2 * _FF), (_FF, _D),
-                  (_B, _HKV, _L, _DH), (_B, _HKV, _L, _DH)],
-    output_shape=(_B, _D),
-    extra_outputs=[dict(shape=(_B, _HKV, _DH), dtype="bf16"),
-                   dict(shape=(_B, _HKV, _DH), dtype="bf16")],
-    rtol=2e-2, atol=2e-2,
-    grid=(1024 * 256, 1, 1),
-    scalars=[dict(binding=10, dtype="u32", value=_B),
-             dict(binding=11, dtype="u32", value=_D),
-             dict(binding=12, dtype="u32", value=_H),
-             dict(binding=13, dtype="u32", value=_HKV),
-             dict(binding=14, dtype="u32", value=_FF),
-             dict(binding=15, dtype="u32", value=_L),
-             dict(binding=16, dtype="f32", value=500000.0),
-             dict(binding=17, dtype="f32", value=1e-5)],
-    # GEMMs 2*B*W, plus q.k and p.v over L+1 positions for every query head.
-    flops=2 * _B * _W + 2 * 2 * _B * _H * (_L + 1) * _DH,
-    # Weights once, KV cache read once, new k/v written, x read and y written.
-    bytes=2 * _W + 2 * 2 * _B * _HKV * _L * _DH + 2 * 2 * _B * _HKV * _DH + 2 * 2 * _B * _D,
-    input_dtypes=["bf16"] * 7,
-    input_init=[("normal", 0.0, 1.0)] + [("normal", 0.0, 0.02)] * 4
-               + [("normal", 0.0, 1.0)] * 2,
-    output_dtype="bf16",
-    compute_dtype="bf16",
-    model_kwargs=dict(B=_B, D=_D, H=_H, H_kv=_HKV, FF=_FF, L=_L, base=500000.0, eps=1e-5),
-    cpu_iters=3,
-)
+def _decode_step(name, B, D, H, HKV, DH, FF, L):
+    QD = H * DH                     # attention width: D for a whole layer
+    QKV = QD + 2 * HKV * DH
+    W = D * QKV + QD * D + D * 2 * FF + FF * D
+    REGISTRY[name] = dict(
+        metal_function="llama_decoder_step_bf16",
+        threadgroup=(256, 1, 1),
+        input_bindings=(0, 1, 2, 3, 4, 5, 6),
+        input_shapes=[(B, D), (D, QKV), (QD, D), (D, 2 * FF), (FF, D),
+                      (B, HKV, L, DH), (B, HKV, L, DH)],
+        output_shape=(B, D),
+        extra_outputs=[dict(shape=(B, HKV, DH), dtype="bf16"),
+                       dict(shape=(B, HKV, DH), dtype="bf16")],
+        rtol=2e-2, atol=2e-2,
+        grid=(1024 * 256, 1, 1),
+        scalars=[dict(binding=10, dtype="u32", value=B),
+                 dict(binding=11, dtype="u32", value=D),
+                 dict(binding=12, dtype="u32", value=H),
+                 dict(binding=13, dtype="u32", value=HKV),
+                 dict(binding=14, dtype="u32", value=FF),
+                 dict(binding=15, dtype="u32", value=L),
+                 dict(binding=16, dtype="f32", value=500000.0),
+                 dict(binding=17, dtype="f32", value=1e-5)],
+        # GEMMs 2*B*W, plus q.k and p.v over L+1 positions for every query head.
+        flops=2 * B * W + 2 * 2 * B * H * (L + 1) * DH,
+        # Weights once, KV cache read once, new k/v written, x read and y written.
+        bytes=2 * W + 2 * 2 * B * HKV * L * DH + 2 * 2 * B * HKV * DH + 2 * 2 * B * D,
+        input_dtypes=["bf16"] * 7,
+        input_init=[("normal", 0.0, 1.0)] + [("normal", 0.0, 0.02)] * 4
+                   + [("normal", 0.0, 1.0)] * 2,
+        output_dtype="bf16",
+        compute_dtype="bf16",
+        model_kwargs=dict(B=B, D=D, H=H, H_kv=HKV, FF=FF, L=L, base=500000.0, eps=1e-5,
+                          D_head=DH),
+        cpu_iters=3,
+    )
+
+
+_decode_step("llama_decoder_step", 16, 4096, 32, 8, 128, 14336, 2048)
+
+# One GPU's share of the same step under 8-way tensor parallelism: 4 of the 32
+# query heads and 1 of the 8 KV heads (W_qkv 4096 x 768), the matching 512
+# rows of W_o, 1792 of the 14336 gate and up columns (W_gu 4096 x 3584) and
+# rows of W_down (1792 x 4096), the KV cache of its head [16, 1, 2048, 128].
+# The step computes exactly that shard's work; the two all-reduces of a
+# 16 x 4096 partial sum (after W_o and after W_down) are not part of it.
+_decode_step("llama_decoder_step_tp8", 16, 4096, 4, 1, 128, 1792, 2048)
 
 # ---- LLaMA decoder layer, prefill, the reference's own shape (fp32) ------------
 # S 64 tokens at positions 0..63, D 128, 4 query heads / 2 KV heads (Dh 32),

@@ -169,29 +169,36 @@ def gqa_decode_attention(q, k_cache, v_cache, k_new, v_new, n_valid=None):
 
 
 def llama_decoder_step(x, w_qkv, w_o, w_gu, w_down, k_cache, v_cache, *, n_heads, n_kv_heads,
-                       pos=None, base=500000.0, eps=1e-5):
+                       pos=None, base=500000.0, eps=1e-5, head_dim=None):
     """One decode step (reference :24-46 applied to one new token per sequence).
 
-    x [B, D]; w_qkv [D, D + 2*Hkv*Dh] columns [Q|K|V]; w_o [D, D];
+    x [B, D]; w_qkv [D, QD + 2*Hkv*Dh] columns [Q|K|V]; w_o [QD, D];
     w_gu [D, 2FF] columns [gate|up]; w_down [FF, D]; caches [B, Hkv, L, Dh]
     holding already-rotated keys of positions 0..L-1.  The new token sits at
-    position L (or `pos`).  Returns (y [B, D], k_new [B, Hkv, Dh], v_new)."""
+    position L (or `pos`).  Returns (y [B, D], k_new [B, Hkv, Dh], v_new).
+
+    QD = n_heads * Dh.  With the default Dh = D / n_heads, QD = D: the
+    reference's layer.  A smaller QD (an explicit `head_dim`) is one
+    tensor-parallel shard of a layer computed alone (its heads, its rows of
+    W_o, its FF columns), i.e. the same formula with the shard's matrices and
+    no all-reduce."""
     x = np.asarray(x, np.float64)
     b, d = x.shape
-    dh = d // n_heads
+    dh = d // n_heads if head_dim is None else head_dim
+    qd = n_heads * dh
     L = k_cache.shape[2]
     pos = L if pos is None else pos
     ff_dim = w_down.shape[0]
 
     h = rms_norm(x, eps)
     qkv = h @ np.asarray(w_qkv, np.float64)
-    q = qkv[:, :d].reshape(b, n_heads, dh)
-    k = qkv[:, d:d + n_kv_heads * dh].reshape(b, n_kv_heads, dh)
-    v = qkv[:, d + n_kv_heads * dh:].reshape(b, n_kv_heads, dh)
+    q = qkv[:, :qd].reshape(b, n_heads, dh)
+    k = qkv[:, qd:qd + n_kv_heads * dh].reshape(b, n_kv_heads, dh)
+    v = qkv[:, qd + n_kv_heads * dh:].reshape(b, n_kv_heads, dh)
     q = rope_interleaved(q, pos, base)
     k = rope_interleaved(k, pos, base)
     attn = gqa_decode_attention(q, k_cache, v_cache, k, v)
-    x1 = x + attn.reshape(b, d) @ np.asarray(w_o, np.float64)
+    x1 = x + attn.reshape(b, qd) @ np.asarray(w_o, np.float64)
     h2 = rms_norm(x1, eps)
     gu = h2 @ np.asarray(w_gu, np.float64)
     act = silu(gu[:, :ff_dim]) * gu[:, ff_dim:]

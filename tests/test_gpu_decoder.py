@@ -22,13 +22,14 @@ RTOL = ATOL = 2e-2
 
 def _make(B, D, H, HKV, FF, L, stride=None, seed=0):
     dh = 128
+    qd = H * dh   # the attention width: D for a whole layer, less for one shard
     stride = stride or L
     s = seed * 100
     bf = "bf16"
     ins = dict(
         x=seeded(s + 1, (B, D), ("normal", 0.0, 1.0), bf),
-        w_qkv=seeded(s + 2, (D, D + 2 * HKV * dh), ("normal", 0.0, 0.02), bf),
-        w_o=seeded(s + 3, (D, D), ("normal", 0.0, 0.02), bf),
+        w_qkv=seeded(s + 2, (D, qd + 2 * HKV * dh), ("normal", 0.0, 0.02), bf),
+        w_o=seeded(s + 3, (qd, D), ("normal", 0.0, 0.02), bf),
         w_gu=seeded(s + 4, (D, 2 * FF), ("normal", 0.0, 0.02), bf),
         w_down=seeded(s + 5, (FF, D), ("normal", 0.0, 0.02), bf),
         k_cache=seeded(s + 6, (B, HKV, stride, dh), ("normal", 0.0, 1.0), bf),
@@ -64,7 +65,8 @@ def _want(ins, H, HKV, L):
     kc = f(ins["k_cache"])[:, :, :L]
     vc = f(ins["v_cache"])[:, :, :L]
     return oracle.llama_decoder_step(f(ins["x"]), f(ins["w_qkv"]), f(ins["w_o"]), f(ins["w_gu"]),
-                                     f(ins["w_down"]), kc, vc, n_heads=H, n_kv_heads=HKV)
+                                     f(ins["w_down"]), kc, vc, n_heads=H, n_kv_heads=HKV,
+                                     head_dim=128)
 
 
 def _check(got, want, what):
@@ -87,6 +89,18 @@ def _check(got, want, what):
 def test_decoder_step_shapes(mb, dev, B, D, H, HKV, FF, L):
     ins = _make(B, D, H, HKV, FF, L)
     _check(_run(dev, ins, B, D, H, HKV, FF, L), _want(ins, H, HKV, L), f"{B,D,H,HKV,FF,L}")
+
+
+@pytest.mark.parametrize("B,D,H,HKV,FF,L", [
+    (16, 4096, 4, 1, 1792, 2048),  # one GPU's share of the registry step at 8-way TP
+    (16, 4096, 8, 2, 3584, 300),   # a 4-way share, ragged cache
+    (3, 1024, 1, 1, 256, 65),      # one head of a layer with D = 1024
+])
+def test_decoder_step_tensor_parallel_shard(mb, dev, B, D, H, HKV, FF, L):
+    """One tensor-parallel shard (attention width H * 128 < D): the shard's
+    QKV columns, W_o rows and FFN slice, all-reduces left to the caller."""
+    ins = _make(B, D, H, HKV, FF, L)
+    _check(_run(dev, ins, B, D, H, HKV, FF, L), _want(ins, H, HKV, L), f"shard {B,D,H,HKV,FF,L}")
 
 
 def test_decoder_step_new_inputs_every_call(mb, dev):
@@ -136,6 +150,8 @@ def test_decoder_step_rejects_bad_shapes(mb, dev):
     a.batch, a.n_kv_heads = 4, 3
     assert lib.mb_launch_llama_decoder_step_bf16(ctypes.byref(a), None) == -7
     a.n_kv_heads, a.cache_stride = 2, 2
+    assert lib.mb_launch_llama_decoder_step_bf16(ctypes.byref(a), None) == -7
+    a.cache_stride, a.d_model = 4, 500          # residual width not a multiple of 128
     assert lib.mb_launch_llama_decoder_step_bf16(ctypes.byref(a), None) == -7
 
 

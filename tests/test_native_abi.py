@@ -80,3 +80,9 @@ def test_decoder_workspace_size_without_gpu():
     assert n >= 56 * 4 * 16 * 512 * 4
     a.head_dim = 64
     assert native.load().mb_decoder_step_workspace_bytes(ctypes.byref(a)) == 0
+    # One 8-way tensor-parallel shard (attention width 4 x 128 < d_model) is a
+    # supported shape; a residual width that is not a multiple of 128 is not.
+    a.head_dim, a.n_heads, a.n_kv_heads, a.d_ff = 128, 4, 1, 1792
+    assert native.load().mb_decoder_step_workspace_bytes(ctypes.byref(a)) > 0, native.last_error()
+    a.d_model = 4000
+    assert native.load().mb_decoder_step_workspace_bytes(ctypes.byref(a)) == 0

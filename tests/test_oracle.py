@@ -294,19 +294,22 @@ def _loop_ffn(x1, w_gu, w_down, eps):
     return np.array(out)
 
 
-def _loop_decoder_step(x, w_qkv, w_o, w_gu, w_down, k_cache, v_cache, H, HKV, base, eps):
+def _loop_decoder_step(x, w_qkv, w_o, w_gu, w_down, k_cache, v_cache, H, HKV, base, eps,
+                       dh=None):
     """One new token per sequence at position L attending to the L cached
-    (already rotated) keys and itself."""
+    (already rotated) keys and itself.  The attention width QD = H * dh is D
+    unless dh is given (one tensor-parallel shard: W_o has QD rows)."""
     B, D = x.shape
-    dh, g, L = D // H, H // HKV, k_cache.shape[2]
+    dh = D // H if dh is None else dh
+    QD, g, L = H * dh, H // HKV, k_cache.shape[2]
     x1, k_new, v_new = [], np.zeros((B, HKV, dh)), np.zeros((B, HKV, dh))
     for b in range(B):
         h = _brute_rms_row(list(x[b]), eps)
         qkv = [sum(h[k] * w_qkv[k, j] for k in range(D)) for j in range(w_qkv.shape[1])]
         for kvh in range(HKV):
-            k_new[b, kvh] = _rot(qkv[D + kvh * dh:D + (kvh + 1) * dh], L, base)
-            v_new[b, kvh] = qkv[D + (HKV + kvh) * dh:D + (HKV + kvh + 1) * dh]
-        att = [0.0] * D
+            k_new[b, kvh] = _rot(qkv[QD + kvh * dh:QD + (kvh + 1) * dh], L, base)
+            v_new[b, kvh] = qkv[QD + (HKV + kvh) * dh:QD + (HKV + kvh + 1) * dh]
+        att = [0.0] * QD
         for hh in range(H):
             kvh = hh // g
             q = _rot(qkv[hh * dh:(hh + 1) * dh], L, base)
@@ -318,7 +321,7 @@ def _loop_decoder_step(x, w_qkv, w_o, w_gu, w_down, k_cache, v_cache, H, HKV, ba
             z = sum(e)
             for dd in range(dh):
                 att[hh * dh + dd] = sum(e[j] / z * vals[j][dd] for j in range(L + 1))
-        x1.append([x[b, j] + sum(att[k] * w_o[k, j] for k in range(D)) for j in range(D)])
+        x1.append([x[b, j] + sum(att[k] * w_o[k, j] for k in range(QD)) for j in range(D)])
     return _loop_ffn(x1, w_gu, w_down, eps), k_new, v_new
 
 
@@ -331,10 +334,12 @@ def _step_inputs(seed=7, B=2, D=16, H=4, HKV=2, FF=6, L=3, scale=0.4):
                 k_cache=n(B, HKV, L, dh), v_cache=n(B, HKV, L, dh))
 
 
-def _step_matches_loops(step_fn, a, H=4, HKV=2, base=500000.0, eps=1e-5):
-    y, kn, vn = step_fn(**a, n_heads=H, n_kv_heads=HKV, base=base, eps=eps)
+def _step_matches_loops(step_fn, a, H=4, HKV=2, base=500000.0, eps=1e-5, dh=None):
+    kw = {} if dh is None else {"head_dim": dh}
+    y, kn, vn = step_fn(**a, n_heads=H, n_kv_heads=HKV, base=base, eps=eps, **kw)
     wy, wk, wv = _loop_decoder_step(*(a[k] for k in ("x", "w_qkv", "w_o", "w_gu", "w_down",
-                                                     "k_cache", "v_cache")), H, HKV, base, eps)
+                                                     "k_cache", "v_cache")), H, HKV, base, eps,
+                                    dh)
     return (np.allclose(y, wy, rtol=1e-10, atol=1e-10) and np.allclose(kn, wk, rtol=1e-10, atol=1e-10)
             and np.allclose(vn, wv, rtol=1e-10, atol=1e-10))
 
@@ -351,6 +356,24 @@ def test_decoder_step_matches_loops():
     assert _step_matches_loops(oracle.llama_decoder_step, _step_inputs())
     assert _step_matches_loops(oracle.llama_decoder_step, _step_inputs(seed=8, H=4, HKV=1, L=5),
                                HKV=1, base=10000.0)
+
+
+def test_decoder_step_tensor_parallel_shard_matches_loops():
+    """One shard of a layer (attention width QD = H * Dh < D: its heads, its
+    QD rows of W_o) against the loop restatement, and the whole-layer width
+    (head_dim = D / H given explicitly) identical to the default."""
+    r = np.random.default_rng(11)
+    B, D, H, HKV, DH, FF, L = 2, 16, 2, 1, 4, 6, 3
+    QD = H * DH
+    n = lambda *s: r.standard_normal(s)  # noqa: E731
+    a = dict(x=n(B, D), w_qkv=n(D, QD + 2 * HKV * DH) * 0.4, w_o=n(QD, D) * 0.4,
+             w_gu=n(D, 2 * FF) * 0.4, w_down=n(FF, D) * 0.4,
+             k_cache=n(B, HKV, L, DH), v_cache=n(B, HKV, L, DH))
+    assert _step_matches_loops(oracle.llama_decoder_step, a, H=H, HKV=HKV, dh=DH)
+    full = _step_inputs()
+    y0, k0, v0 = oracle.llama_decoder_step(**full, n_heads=4, n_kv_heads=2)
+    y1, k1, v1 = oracle.llama_decoder_step(**full, n_heads=4, n_kv_heads=2, head_dim=4)
+    assert np.array_equal(y0, y1) and np.array_equal(k0, k1) and np.array_equal(v0, v1)
 
 
 def test_decoder_step_ffn_half_with_zero_w_o():
