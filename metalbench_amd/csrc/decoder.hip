@@ -870,10 +870,16 @@ struct Plan {
 // K split of a skinny GEMM: enough splits that tiles x splits gives about one
 // workgroup per CU (fewer, longer streams read HBM faster than two per CU),
 // each split a whole number of 32-row groups (so 5 splits of K = 4096 are
-// 832, 832, 832, 832 and 768 rows rather than 7, 7, 7, 7 and 4 steps of 128);
-// the ring holds RING units of 128 / ww rows, or the split's unit count below
-// that.
-constexpr uint32_t KG = 32;   // K split granularity (rows)
+// 832, 832, 832, 832 and 768 rows rather than 7, 7, 7, 7 and 4 steps of 128)
+// and at least MIN_KC rows: a tile's last workgroup reads every split's
+// partial sums, and on the small GEMMs of one 8-way tensor-parallel shard
+// (qkv: 6 column tiles, K = 4096; W_o: K = 512) splits of 64-128 rows made
+// that reduction the larger part of the kernel (qkv 13.9 -> 11.6 us, W_o
+// 9.7 -> 9.4 us at 256 rows; 384 and 512 were slower). The full layer's
+// splits are all 512 rows or more, so this leaves its plan unchanged. The
+// ring holds RING units of 128 / ww rows, or the split's unit count below that.
+constexpr uint32_t KG = 32;       // K split granularity (rows)
+constexpr uint32_t MIN_KC = 256;  // fewest K rows per split
 
 // The plan is a function of the shapes alone: it is sized for the 256 CUs of
 // a whole gfx950 device (MI350X / MI355X), not for the device in use, so
@@ -887,7 +893,8 @@ static void choose_split(uint32_t tiles, uint32_t k, uint32_t ww, uint32_t* spli
                          uint32_t* ring) {
     const uint32_t groups = k / KG;
     const uint32_t slots = PLAN_CUS;
-    const uint32_t want = std::min(std::max(1u, slots / tiles), groups);
+    const uint32_t want =
+        std::min(std::max(1u, slots / tiles), std::max(1u, groups / (MIN_KC / KG)));
     const uint32_t per = cdiv(groups, want);
     *splits = cdiv(groups, per);
     *kc = per * KG;
@@ -945,8 +952,12 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
     pl->tiles[EPI_QKV] = pl->nqkv / BN;
     pl->tiles[EPI_WO] = D / BN;
     // W_gate | W_up in 512-column tiles (1 KB row segments) when d_ff allows
+    // and there are at least PLAN_CUS / 8 of them. With fewer (d_ff = 1792 of
+    // an 8-way shard has 7) each tile is split 32 ways and its last workgroup
+    // sums 4 x 32 partial tiles, 1 MB: 27.0 us against 14.3 us for the 28
+    // 128-column tiles.
     pl->ww[EPI_QKV] = pl->ww[EPI_WO] = pl->ww[EPI_DOWN] = 1;
-    pl->ww[EPI_GU] = FF % (2 * BN) == 0 ? 4 : 1;
+    pl->ww[EPI_GU] = FF % (2 * BN) == 0 && FF / (2 * BN) >= PLAN_CUS / 8 ? 4 : 1;
     pl->tiles[EPI_GU] = FF / (BN / 2 * pl->ww[EPI_GU]);
     pl->tiles[EPI_DOWN] = D / BN;
     const uint32_t ldw[4] = {pl->nqkv, D, 2 * FF, D};
