@@ -62,7 +62,9 @@ def _step_shape(meta: dict) -> dict:
 def _decoder_part_bytes(meta: dict | None = None) -> dict:
     """Algorithmic HBM bytes of one launch of each decoder kernel: every weight
     and cache byte once, activations in and out once (bf16 = 2 bytes).  The
-    attention width QD = H * Dh is D for a whole layer."""
+    attention width QD = H * Dh is D for a whole layer.  The QKV GEMM's
+    outputs reach the attention kernel as split-K partials (workspace traffic,
+    not counted)."""
     if meta is None:
         from metalbench_amd import helpers as H
         meta = H.load_baseline("llama_decoder_step").meta
@@ -71,8 +73,8 @@ def _decoder_part_bytes(meta: dict | None = None) -> dict:
     QD = t["H"] * DH
     qkv_n = QD + 2 * HKV * DH
     return {
-        "qkv_rope": 2 * (D * qkv_n + B * D + B * QD + 2 * B * HKV * DH),
-        "attention": 2 * (2 * B * HKV * L * DH + B * QD),
+        "qkv": 2 * (D * qkv_n + B * D),
+        "attention": 2 * (2 * B * HKV * L * DH + 2 * B * HKV * DH + B * QD),
         "wo_residual": 2 * (QD * D + B * QD + B * D) + 4 * B * D,
         "gate_up_swiglu": 2 * (D * 2 * FF + B * D + B * FF),
         "down_residual": 2 * (FF * D + B * FF + B * D) + 4 * B * D,
@@ -88,7 +90,7 @@ def _work(name: str, meta: dict):
         # per-kernel figures stay in `parts`.
         parts = _decoder_part_bytes(meta)
         return dict(part=None, bound="hbm", per_launch=sum(parts.values()), parts=parts,
-                    label="decode step: qkv_rope, attention, wo_residual, gate_up_swiglu, "
+                    label="decode step: qkv, attention, wo_residual, gate_up_swiglu, "
                           "down_residual")
     if _bound(meta) == "hbm":
         return dict(part=None, bound="hbm", per_launch=int(meta["bytes"]))

@@ -12,14 +12,17 @@
 // The step is HBM bound (436 MB of weights + 134 MB of KV cache per step at
 // B = 16, L = 2048 against ~7.5 GFLOP), so every kernel is shaped to stream
 // its bytes once:
-//   1. qkv_rope       skinny GEMM x @ W_qkv, finisher applies the RMSNorm row
-//                     scale (sum of squares gathered from the A operand for
-//                     free), RoPE, writes q (bf16, pre-scaled by 1/sqrt(Dh))
-//                     and k_new / v_new (bf16);
+//   1. qkv            skinny GEMM x @ W_qkv that leaves its split-K partials
+//                     and per-split sums of x^2 (gathered from the A operand
+//                     for free); no finisher;
 //   2. attention      flash-decoding: one workgroup per (sequence, kv head,
-//                     split of the cached keys); q.k^T on MFMA, online
-//                     softmax, p.v on VALU; the last split to finish merges
-//                     the splits and the new token (log-sum-exp);
+//                     split of the cached keys).  Its prologue sums the QKV
+//                     partials of its heads, applies the RMSNorm row scale
+//                     and RoPE (q pre-scaled by 1/sqrt(Dh), bf16; k_new and
+//                     v_new bf16, written out by split 0) while the first
+//                     K/V block is in flight; q.k^T on MFMA, online softmax,
+//                     p.v on VALU; the last split to finish merges the splits
+//                     and the new token (log-sum-exp);
 //   3. wo_residual    skinny GEMM attn @ W_o, finisher adds x, writes x1
 //                     (fp32 + bf16) and per-tile sums of x1^2;
 //   4. gate_up_swiglu skinny GEMM x1 @ [W_gate | W_up], each tile holding 256
@@ -39,7 +42,9 @@
 // once per step).  Split-K partials go to the workspace and the LAST
 // workgroup of each column tile (an atomic counter, reset by that workgroup)
 // sums them in split order and runs the epilogue; the partials travel through
-// device-coherent (sc1) accesses, not fences.  Details at skinny_gemm_kernel.
+// device-coherent (sc1) accesses, not fences.  The QKV GEMM has no finisher:
+// its partials are summed, in the same order, by the attention kernel that
+// reads them.  Details at skinny_gemm_kernel.
 #include "common.h"
 
 #include <math.h>
@@ -153,8 +158,9 @@ struct StepParams {
     uint32_t* attn_counters;   // [B * Hkv]
     float* partial;            // split-K partials [tiles * splits][16][tile columns]
     uint32_t partial_bytes;
-    float* sumsq;              // [qkv tiles * splits][16] sum of x^2 over each split
-    uint16_t* q;               // [B][QD] rotated queries * 1/sqrt(Dh), bf16 (MFMA operand)
+    float* sumsq;              // [qkv splits][16] sum of x^2 over each split
+    uint32_t qkv_splits;       // K splits of the QKV GEMM (its partials' split count)
+    float* rope;               // [Dh / 2][2] cos, sin of pair i at position cache_len
     float* attn_part;          // [B][Hkv][nsplit][G][DH + 4]  (o[DH], m, l, pad)
     uint32_t attn_part_bytes;
     uint32_t sumsq_bytes;
@@ -214,7 +220,8 @@ struct GemmCfg {
 // (the 4 / WW row groups summed); the split-K partial in the workspace has the
 // same layout (one coalesced sc1 store per float4).  The last workgroup of
 // the tile (atomic counter) sums the other splits' partials, with the
-// epilogue's own inputs loaded in the same round trip, and runs the epilogue.
+// epilogue's own inputs loaded in the same round trip, and runs the epilogue
+// (W_o, gate/up, down; the QKV partials are summed by the attention kernel).
 template <int TBN>
 __device__ __forceinline__ uint32_t tile_col(const GemmCfg& g, const StepParams& p, uint32_t tile,
                                              uint32_t c) {
@@ -278,16 +285,18 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
         issue(s, s);
         __builtin_amdgcn_sched_barrier(0);
     }
-    // QKV: the RoPE rotation of pair (2i, 2i+1), i = tid % 64, at position
-    // cache_len, computed while the first loads are in flight.  The angle
-    // pos * base^(-2i/Dh) is formed and reduced mod 2 pi in fp64: an fp32
-    // angle would be off by ~pos * 6e-8 rad (0.06 rad at pos 10^6).
-    float rope_cs = 1.f, rope_sn = 0.f;
-    if (EPI == EPI_QKV) {
-        const double omega = pow((double)p.rope_base, -2.0 * (double)(tid & 63) / (double)DH);
+    // QKV: workgroup 0 writes the RoPE table (cos, sin) of pair (2i, 2i+1),
+    // i = tid < 64, at position cache_len, for the attention kernel, while
+    // its first loads are in flight.  The angle pos * base^(-2i/Dh) is formed
+    // and reduced mod 2 pi in fp64: an fp32 angle would be off by
+    // ~pos * 6e-8 rad (0.06 rad at pos 10^6).
+    if (EPI == EPI_QKV && blockIdx.x == 0 && tid < DH / 2) {
+        const double omega = pow((double)p.rope_base, -2.0 * (double)tid / (double)DH);
         const double ang = (double)p.cache_len * omega;
         constexpr double TWO_PI = 6.283185307179586476925;
-        sincosf((float)(ang - TWO_PI * rint(ang / TWO_PI)), &rope_sn, &rope_cs);
+        float cs, sn;
+        sincosf((float)(ang - TWO_PI * rint(ang / TWO_PI)), &sn, &cs);
+        *reinterpret_cast<float2*>(p.rope + 2 * tid) = float2{cs, sn};
     }
 
     f32x4 acc[8];
@@ -366,38 +375,32 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
 #pragma unroll
     for (int h = 0; h < NQ; ++h) st_sc1(prs, tile_base + split * SPLIT_BYTES + (tid + 256 * h) * 16, v[h]);
     const __amdgpu_buffer_rsrc_t srs = coherent_rsrc(p.sumsq, p.sumsq_bytes);
-    if (EPI == EPI_QKV && tid < MROWS) {
+    if (EPI == EPI_QKV && tile == 0 && tid < MROWS) {   // every tile sums the same x rows
         const float* sp = red + RG * MROWS * TBN;
-        st_sc1(srs, ((tile * g.splits + split) * MROWS + tid) * 4,
+        st_sc1(srs, (split * MROWS + tid) * 4,
                sp[tid] + sp[MROWS + tid] + sp[2 * MROWS + tid] + sp[3 * MROWS + tid]);
     }
+    // QKV: no finisher; each attention workgroup sums the partials it needs.
+    if (EPI == EPI_QKV) return;
     if (!arrive_last(&g.counters[tile], g.splits, &s_last)) return;
 
     // ---- finisher: this workgroup is the last of its tile ----
-    // One memory round trip: the first SB splits' partials, the QKV split sums
-    // of x^2 and the epilogue's inputs are all issued before the first wait.
+    // One memory round trip: the first SB splits' partials and the epilogue's
+    // inputs are all issued before the first wait.
     // Partials and sums are read through descriptors clipped to this tile's
     // splits, so loads past the last split return zeros and every load and
     // add is unconditional (a load behind a branch would cost a round trip of
     // its own).  Splits are summed in split order whichever workgroup
     // finishes, so the result does not depend on arrival order.
     constexpr uint32_t SB = NQ >= 8 ? 4 : 8;   // splits per batch of partial loads
-    constexpr uint32_t UT = 8;                 // QKV: x^2 sums per thread per batch
     const __amdgpu_buffer_rsrc_t trs = coherent_rsrc(
         reinterpret_cast<const uint8_t*>(p.partial) + tile_base, g.splits * SPLIT_BYTES);
-    const __amdgpu_buffer_rsrc_t qrs =
-        coherent_rsrc(p.sumsq + tile * g.splits * MROWS, g.splits * MROWS * 4);
-    const uint32_t row = tid & 15, grp = tid >> 4;   // row statistics: row, group of splits
+    const uint32_t row = tid & 15, grp = tid >> 4;   // row statistics: row, group of tiles
     f32x4 w[SB][NQ];
 #pragma unroll
     for (uint32_t u = 0; u < SB; ++u)
 #pragma unroll
         for (int h = 0; h < NQ; ++h) w[u][h] = ld4_sc1(trs, u * SPLIT_BYTES + (tid + 256 * h) * 16);
-    float xs[UT] = {};
-    if (EPI == EPI_QKV) {
-#pragma unroll
-        for (uint32_t u = 0; u < UT; ++u) xs[u] = ld_sc1(qrs, ((grp + 16 * u) * MROWS + row) * 4);
-    }
     const uint32_t eb = tid >> 4, ec = 8 * (tid & 15);   // epilogue: row eb, columns ec .. ec+7
     u32x4 pre_x = {};                                    // WO: x (bf16)
     f32x4 pre_x1[2] = {f32x4{}, f32x4{}};                // DOWN: x1 (fp32)
@@ -438,67 +441,27 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
 #pragma unroll
         for (int h = 0; h < NQ; ++h) reinterpret_cast<f32x4*>(red)[tid + 256 * h] = sum[h];
     }
-    // Row statistics, thread (row, grp) summing every 16th term, then the 16
-    // groups through LDS:
-    //   QKV: sum of x^2 over the splits;
-    //   GU:  sum of x1^2 over the W_o column tiles -> RMSNorm scale.
-    if (EPI == EPI_QKV || EPI == EPI_GU) {
+    // GU: the RMSNorm scale of x1, from the sums of x1^2 over the W_o column
+    // tiles: thread (row, grp) sums every 16th tile, then the 16 groups
+    // through LDS.
+    if (EPI == EPI_GU) {
         float* scratch = red + MROWS * TBN;   // 16 x 16 floats past the tile sums
         float sv = 0.f;
-        if (EPI == EPI_QKV) {
 #pragma unroll
-            for (uint32_t u = 0; u < UT; ++u) sv += xs[u];
-            for (uint32_t t0 = 16 * UT; t0 < g.splits; t0 += 16 * UT) {   // more than 128 splits
-#pragma unroll
-                for (uint32_t u = 0; u < UT; ++u)
-                    xs[u] = ld_sc1(qrs, ((t0 + grp + 16 * u) * MROWS + row) * 4);
-#pragma unroll
-                for (uint32_t u = 0; u < UT; ++u) sv += xs[u];
-            }
-        } else {
-#pragma unroll
-            for (uint32_t u = 0; u < 8; ++u)
-                if (grp + 16 * u < p.d / 128) sv += pre_ss[u];
-        }
+        for (uint32_t u = 0; u < 8; ++u)
+            if (grp + 16 * u < p.d / 128) sv += pre_ss[u];
         scratch[grp * MROWS + row] = sv;
         __syncthreads();
         if (tid < MROWS) {
             float t = 0.f;
 #pragma unroll
             for (int q = 0; q < 16; ++q) t += scratch[q * MROWS + tid];
-            red_ss[tid] = EPI == EPI_QKV ? t : rsqrtf(t / (float)p.d + p.eps);
+            red_ss[tid] = rsqrtf(t / (float)p.d + p.eps);
         }
     }
     __syncthreads();
 
-    if (EPI == EPI_QKV) {
-        // Tile = one head of Q, K or V (all three regions are multiples of 128).
-        const uint32_t base = tile * TBN;
-        const uint32_t i = tid & 63;                       // rotation pair (2i, 2i+1)
-        const float cs = rope_cs, sn = rope_sn;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            const uint32_t b = 4 * (tid >> 6) + rr;
-            if (b >= p.batch) continue;
-            const float r1 = rsqrtf(red_ss[b] / (float)p.d + p.eps);
-            const float2 vv = *reinterpret_cast<const float2*>(&red[b * TBN + 2 * i]);
-            const float v0 = vv.x * r1, v1 = vv.y * r1;
-            if (base < p.qd) {
-                // pre-scaled by 1/sqrt(Dh) and rounded once for the q.k^T MFMA
-                const float qs = rsqrtf((float)DH);
-                *reinterpret_cast<uint32_t*>(p.q + (size_t)b * p.qd + base + 2 * i) =
-                    pack_bf16((v0 * cs - v1 * sn) * qs, (v0 * sn + v1 * cs) * qs);
-            } else if (base < p.qd + p.hkv * DH) {
-                const uint32_t kvh = (base - p.qd) / DH;
-                *reinterpret_cast<uint32_t*>(p.k_new + ((size_t)b * p.hkv + kvh) * DH + 2 * i) =
-                    pack_bf16(v0 * cs - v1 * sn, v0 * sn + v1 * cs);
-            } else {
-                const uint32_t kvh = (base - p.qd - p.hkv * DH) / DH;
-                *reinterpret_cast<uint32_t*>(p.v_new + ((size_t)b * p.hkv + kvh) * DH + 2 * i) =
-                    pack_bf16(v0, v1);
-            }
-        }
-    } else if (EPI == EPI_WO) {
+    if (EPI == EPI_WO) {
         // thread: row eb, columns ec .. ec+7; x1 = x + attn W_o (rows past
         // the batch computed from x row 0, never stored, their sums zeroed)
         const f32x4 r0 = *reinterpret_cast<const f32x4*>(&red[eb * TBN + ec]);
@@ -610,7 +573,8 @@ struct KVBlock {
 template <int GT>
 __global__ __launch_bounds__(256)
 void attention_kernel(StepParams p) {
-    __shared__ uint16_t qs[16][QP];        // q rows of this kv head (rows past G zero)
+    __shared__ __attribute__((aligned(16))) uint16_t qs[16][QP];   // q rows (rows past G zero)
+    __shared__ __attribute__((aligned(16))) uint16_t kvn[2][DH];   // k_new, v_new (bf16)
     // per wave: p[key][head] of the current block.  Row pitch 20 floats: the
     // store of lane (j, grp), row 4 grp + r, lands in bank 16 grp + 20 r + j,
     // so the 64 lanes hit 64 banks (with a pitch of 16 the four grp rows were
@@ -641,8 +605,6 @@ void attention_kernel(StepParams p) {
     const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
         uniform_ptr(nkeys ? p.v_cache + row0 * DH : p.v_new), 0,
         __builtin_amdgcn_readfirstlane(nkeys * DH * 2), RSRC_FLAGS);
-    const uint16_t* knew = p.k_new + (size_t)bk * DH;
-    const uint16_t* vnew = p.v_new + (size_t)bk * DH;
 
     // Offsets (bytes) inside the split of this lane's first K and V dwords.
     const uint32_t koff = ((16 * wave + j) * DH + 8 * grp) * 2;
@@ -657,19 +619,122 @@ void attention_kernel(StepParams p) {
             blk.v[i] = __builtin_amdgcn_raw_buffer_load_b32(vrs, base + voff + i * DH * 2, 0, CPOL_NT);
     };
 
-    // q rows of the G heads go to LDS (the MFMA B operand is re-read per
-    // block); their loads are issued ahead of the first K/V block.
-    static_assert(16 * (DH / 8) == 256, "one 16-byte q chunk per thread");
-    const uint32_t qh = tid / (DH / 8), qc = tid % (DH / 8);
-    const u32x4 qv = *reinterpret_cast<const u32x4*>(
-        p.q + (size_t)b * p.qd + (kvh * G + (qh < G ? qh : 0)) * DH + 8 * qc);
+    // ---- q, the new key and the new value of this (sequence, kv head) ----
+    // The QKV GEMM leaves split-K partials, [tile][split][16][128] fp32 with
+    // tile = one head of Q, K or V, and per-split row sums of x^2.  Every
+    // workgroup of the pair sums row b of its G query heads, its key head and
+    // its value head over the splits (left to right, in batches of 8: loads
+    // past the last split return zeros), applies the RMSNorm row scale and
+    // the RoPE rotation, and keeps q (pre-scaled by 1/sqrt(Dh), the MFMA B
+    // operand, re-read per block), k_new and v_new as bf16 in LDS.  These
+    // loads go out ahead of the first K/V block's, which do not depend on
+    // them; split 0 also writes k_new and v_new out.
+    constexpr uint32_t SPLIT_BYTES = MROWS * DH * 4;
+    constexpr uint32_t PB = 16;   // splits loaded ahead of the first K/V block
+    const uint32_t qsp = p.qkv_splits;
+    const uint32_t nitems_q = (G + 2) * (DH / 4);           // (head, column quad) items
+    const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+        p.sumsq, 0, __builtin_amdgcn_readfirstlane(qsp * MROWS * 4), RSRC_FLAGS);
+    const __amdgpu_buffer_rsrc_t prs =
+        __builtin_amdgcn_make_buffer_rsrc(p.partial, 0, p.partial_bytes, RSRC_FLAGS);
+    auto item_base = [&](uint32_t idx) -> uint32_t {
+        const uint32_t ts = idx / (DH / 4), c = idx % (DH / 4);
+        const uint32_t tile = ts < G ? kvh * G + ts : p.qd / DH + (ts - G) * p.hkv + kvh;
+        return tile * qsp * SPLIT_BYTES + b * (DH * 4) + 16 * c;
+    };
+    f32x4 pw[PB];
+    auto load_item = [&](uint32_t base, uint32_t c0) {
+#pragma unroll
+        for (uint32_t u = 0; u < PB; ++u)
+            pw[u] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           prs, c0 + u < qsp ? base + (c0 + u) * SPLIT_BYTES : 0x80000000u, 0, 0));
+    };
+    // The splits are summed left to right: sum = w0 + w1 + ... (loads past
+    // the last split add zeros).
+    auto sum_item = [&](uint32_t base) -> f32x4 {
+        f32x4 sum = pw[0];
+#pragma unroll
+        for (uint32_t u = 1; u < PB; ++u) sum += pw[u];
+        for (uint32_t c0 = PB; c0 < qsp; c0 += PB) {   // more splits: loads after the K/V block's
+            load_item(base, c0);
+#pragma unroll
+            for (uint32_t u = 0; u < PB; ++u) sum += pw[u];
+        }
+        return sum;
+    };
+    // row b's sum of x^2: lane l < 16 of each wave sums splits l, l + 16, ...,
+    // then the 16 lanes are added in order
+    constexpr uint32_t XB = 8;
+    float xs[XB];
+    auto load_xs = [&](uint32_t t0) {
+#pragma unroll
+        for (uint32_t u = 0; u < XB; ++u)
+            xs[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                srs, lane < 16 ? ((t0 + lane + 16 * u) * MROWS + b) * 4 : 0x80000000u, 0, 0));
+    };
+    // Every load the first item needs is issued before the first K/V block's
+    // (vmcnt retires loads in issue order: a wait for a later load would also
+    // wait for that block and delay the next block's issue).
+    const uint32_t item0 = min(tid, nitems_q - 1);
+    const uint32_t base0 = item_base(item0);
+    load_xs(0);
+    load_item(base0, 0);
+    const f32x4 rope0 = *reinterpret_cast<const f32x4*>(p.rope + 4 * (item0 % (DH / 4)));
     KVBlock kv[AR];
 #pragma unroll
     for (int u = 0; u < AR - 1; ++u) {
         load(kv[u], u);
         __builtin_amdgcn_sched_barrier(0);
     }
-    *reinterpret_cast<u32x4*>(&qs[qh][8 * qc]) = qh < G ? qv : u32x4{};
+    float r1;
+    {
+        float sv = 0.f;
+#pragma unroll
+        for (uint32_t u = 0; u < XB; ++u) sv += xs[u];
+        for (uint32_t t0 = 16 * XB; t0 < qsp; t0 += 16 * XB) {   // more than 128 splits
+            load_xs(t0);
+#pragma unroll
+            for (uint32_t u = 0; u < XB; ++u) sv += xs[u];
+        }
+        float t = 0.f;
+#pragma unroll
+        for (int l = 0; l < 16; ++l)
+            t += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), l));
+        r1 = rsqrtf(t / (float)p.d + p.eps);
+    }
+    auto finish_item = [&](uint32_t idx, f32x4 sum, f32x4 rt) {
+        const uint32_t ts = idx / (DH / 4), c = idx % (DH / 4);
+        const float v0 = sum[0] * r1, v1 = sum[1] * r1, v2 = sum[2] * r1, v3 = sum[3] * r1;
+        uint2 out;
+        if (ts < G) {
+            const float qsc = rsqrtf((float)DH);
+            out.x = pack_bf16((v0 * rt[0] - v1 * rt[1]) * qsc, (v0 * rt[1] + v1 * rt[0]) * qsc);
+            out.y = pack_bf16((v2 * rt[2] - v3 * rt[3]) * qsc, (v2 * rt[3] + v3 * rt[2]) * qsc);
+            *reinterpret_cast<uint2*>(&qs[ts][4 * c]) = out;
+        } else {
+            if (ts == G) {
+                out.x = pack_bf16(v0 * rt[0] - v1 * rt[1], v0 * rt[1] + v1 * rt[0]);
+                out.y = pack_bf16(v2 * rt[2] - v3 * rt[3], v2 * rt[3] + v3 * rt[2]);
+            } else {
+                out.x = pack_bf16(v0, v1);
+                out.y = pack_bf16(v2, v3);
+            }
+            *reinterpret_cast<uint2*>(&kvn[ts - G][4 * c]) = out;
+            if (split == 0)
+                *reinterpret_cast<uint2*>((ts == G ? p.k_new : p.v_new) + (size_t)bk * DH + 4 * c) = out;
+        }
+    };
+    if (tid < nitems_q) finish_item(tid, sum_item(base0), rope0);
+    for (uint32_t idx = tid + 256; idx < nitems_q; idx += 256) {   // G > 4: more items
+        const uint32_t base = item_base(idx);
+        load_item(base, 0);
+        finish_item(idx, sum_item(base), *reinterpret_cast<const f32x4*>(p.rope + 4 * (idx % (DH / 4))));
+    }
+    {   // query rows past G are zero
+        const uint32_t qh = tid / (DH / 8), qc = tid % (DH / 8);
+        if (qh >= G) *reinterpret_cast<u32x4*>(&qs[qh][8 * qc]) = u32x4{};
+    }
     __syncthreads();
 
     float m_run = NEG_BIG, l_run = 0.f;   // lane (j, grp): head j; l over this lane's keys
@@ -802,14 +867,13 @@ void attention_kernel(StepParams p) {
         }
     };
     load_batch(min(tid, nitems - 1), 0);
-    const uint2 vv0 = *reinterpret_cast<const uint2*>(vnew + 4 * (tid % (DH / 4)));
+    const uint2 vv0 = *reinterpret_cast<const uint2*>(&kvn[1][4 * (tid % (DH / 4))]);
     {   // s_new = q . k_new (q is pre-scaled); wave w takes heads w, w + 4, ...
-        const uint32_t ka = *reinterpret_cast<const uint32_t*>(knew + 2 * lane);
+        const uint32_t ka = *reinterpret_cast<const uint32_t*>(&kvn[0][2 * lane]);
         uint32_t qa[GT / 4];
 #pragma unroll
         for (int i = 0; i < GT / 4; ++i)
-            qa[i] = *reinterpret_cast<const uint32_t*>(
-                p.q + (size_t)b * p.qd + (kvh * G + min(wave + 4 * i, G - 1)) * DH + 2 * lane);
+            qa[i] = *reinterpret_cast<const uint32_t*>(&qs[min(wave + 4 * i, G - 1)][2 * lane]);
 #pragma unroll
         for (int i = 0; i < GT / 4; ++i) {
             float d = __uint_as_float(qa[i] << 16) * __uint_as_float(ka << 16) +
@@ -845,7 +909,7 @@ void attention_kernel(StepParams p) {
         const float Mf = fmaxf(M, sn);
         const float so = __builtin_amdgcn_exp2f((M - Mf) * LOG2E);
         const float wn = __builtin_amdgcn_exp2f((sn - Mf) * LOG2E);
-        const uint2 vv = idx == tid ? vv0 : *reinterpret_cast<const uint2*>(vnew + 4 * d4);
+        const uint2 vv = idx == tid ? vv0 : *reinterpret_cast<const uint2*>(&kvn[1][4 * d4]);
         const f32x4 vn = {__uint_as_float(vv.x << 16), __uint_as_float(vv.x & 0xffff0000u),
                           __uint_as_float(vv.y << 16), __uint_as_float(vv.y & 0xffff0000u)};
         const f32x4 res = (O * so + wn * vn) / (L * so + wn);
@@ -862,9 +926,9 @@ void attention_kernel(StepParams p) {
 struct Plan {
     uint32_t nqkv, g, nsplit, split_keys;
     uint32_t tiles[4], splits[4], kc[4], ring[4], ww[4];
-    size_t off_counters, off_partial, off_sumsq, off_q, off_attn_part, off_attn_out, off_x1,
+    size_t off_counters, off_partial, off_sumsq, off_rope, off_attn_part, off_attn_out, off_x1,
         off_x1b, off_x1b_lo, off_sumsq2, off_act, off_act_lo, total;
-    uint32_t counter_base[5];   // qkv, attn, wo, gu, down
+    uint32_t counter_base[4];   // attn, wo, gu, down (the QKV GEMM has no finisher)
 };
 
 // K split of a skinny GEMM: enough splits that tiles x splits gives about one
@@ -974,18 +1038,17 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
     size_t max_part = 0;
     for (int i = 0; i < 4; ++i)
         max_part = std::max(max_part, (size_t)pl->tiles[i] * pl->splits[i] * pl->ww[i]);
-    const uint32_t n_counters = pl->tiles[EPI_QKV] + B * a->n_kv_heads + pl->tiles[EPI_WO] +
-                                pl->tiles[EPI_GU] + pl->tiles[EPI_DOWN];
+    const uint32_t n_counters =
+        B * a->n_kv_heads + pl->tiles[EPI_WO] + pl->tiles[EPI_GU] + pl->tiles[EPI_DOWN];
     pl->counter_base[0] = 0;
-    pl->counter_base[1] = pl->tiles[EPI_QKV];
-    pl->counter_base[2] = pl->counter_base[1] + B * a->n_kv_heads;
-    pl->counter_base[3] = pl->counter_base[2] + pl->tiles[EPI_WO];
-    pl->counter_base[4] = pl->counter_base[3] + pl->tiles[EPI_GU];
+    pl->counter_base[1] = pl->counter_base[0] + B * a->n_kv_heads;
+    pl->counter_base[2] = pl->counter_base[1] + pl->tiles[EPI_WO];
+    pl->counter_base[3] = pl->counter_base[2] + pl->tiles[EPI_GU];
     size_t o = 0;
     pl->off_counters = o; o = align256(o + (size_t)n_counters * 4);
     pl->off_partial = o; o = align256(o + max_part * MROWS * BN * 4);
-    pl->off_sumsq = o; o = align256(o + (size_t)pl->tiles[EPI_QKV] * pl->splits[EPI_QKV] * MROWS * 4);
-    pl->off_q = o; o = align256(o + (size_t)B * QD * 2);
+    pl->off_sumsq = o; o = align256(o + (size_t)pl->splits[EPI_QKV] * MROWS * 4);
+    pl->off_rope = o; o = align256(o + DH / 2 * 2 * 4);
     pl->off_attn_part = o;
     o = align256(o + (size_t)B * a->n_kv_heads * pl->nsplit * pl->g * APITCH * 4);
     pl->off_attn_out = o; o = align256(o + (size_t)B * QD * 2);
@@ -1055,13 +1118,14 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
     p.x = a->x; p.k_cache = a->k_cache; p.v_cache = a->v_cache;
     p.y = a->y; p.k_new = a->k_new; p.v_new = a->v_new;
     uint32_t* counters = reinterpret_cast<uint32_t*>(ws + pl.off_counters);
-    p.attn_counters = counters + pl.counter_base[1];
+    p.attn_counters = counters + pl.counter_base[0];
     p.partial = reinterpret_cast<float*>(ws + pl.off_partial);
     p.partial_bytes = (uint32_t)(pl.off_sumsq - pl.off_partial);
-    p.sumsq_bytes = (uint32_t)(pl.off_q - pl.off_sumsq);
+    p.sumsq_bytes = (uint32_t)(pl.off_rope - pl.off_sumsq);
     p.attn_part_bytes = (uint32_t)(pl.off_attn_out - pl.off_attn_part);
     p.sumsq = reinterpret_cast<float*>(ws + pl.off_sumsq);
-    p.q = reinterpret_cast<uint16_t*>(ws + pl.off_q);
+    p.rope = reinterpret_cast<float*>(ws + pl.off_rope);
+    p.qkv_splits = pl.splits[EPI_QKV];
     p.attn_part = reinterpret_cast<float*>(ws + pl.off_attn_part);
     p.attn_out = reinterpret_cast<uint16_t*>(ws + pl.off_attn_out);
     p.x1 = reinterpret_cast<float*>(ws + pl.off_x1);
@@ -1082,18 +1146,18 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
         return g;
     };
     const GemmCfg g_qkv =
-        gemm(EPI_QKV, a->x, nullptr, D, a->w_qkv, pl.nqkv, D, pl.counter_base[0]);
+        gemm(EPI_QKV, a->x, nullptr, D, a->w_qkv, pl.nqkv, D, 0);   // (no counters)
     const GemmCfg g_wo =
-        gemm(EPI_WO, p.attn_out, nullptr, QD, a->w_o, D, QD, pl.counter_base[2]);
+        gemm(EPI_WO, p.attn_out, nullptr, QD, a->w_o, D, QD, pl.counter_base[1]);
     const GemmCfg g_gu =
-        gemm(EPI_GU, p.x1b, p.x1b_lo, D, a->w_gu, 2 * FF, D, pl.counter_base[3]);
+        gemm(EPI_GU, p.x1b, p.x1b_lo, D, a->w_gu, 2 * FF, D, pl.counter_base[2]);
     const GemmCfg g_dn =
-        gemm(EPI_DOWN, p.act, p.act_lo, FF, a->w_down, D, FF, pl.counter_base[4]);
+        gemm(EPI_DOWN, p.act, p.act_lo, FF, a->w_down, D, FF, pl.counter_base[3]);
 
     auto mark = [&](const char* name) { if (pm) pm->mark(s, name); };
-    mark("qkv_rope");
+    mark("qkv");
     launch_skinny<EPI_QKV>(g_qkv, pl, p, s);
-    MB_LAUNCH_CHECK("decoder qkv_rope");
+    MB_LAUNCH_CHECK("decoder qkv");
     mark("attention");
     {
         const dim3 grid(a->batch * a->n_kv_heads * pl.nsplit), block(256);
