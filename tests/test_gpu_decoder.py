@@ -95,6 +95,8 @@ def test_decoder_step_shapes(mb, dev, B, D, H, HKV, FF, L):
     (16, 4096, 4, 1, 1792, 2048),  # one GPU's share of the registry step at 8-way TP
     (16, 4096, 8, 2, 3584, 300),   # a 4-way share, ragged cache
     (3, 1024, 1, 1, 256, 65),      # one head of a layer with D = 1024
+    (2, 8192, 1, 1, 256, 64),      # 32 QKV K splits: the attention prologue sums two batches
+    (1, 16384, 1, 1, 128, 16),     # 64 QKV K splits, the widest d_model
 ])
 def test_decoder_step_tensor_parallel_shard(mb, dev, B, D, H, HKV, FF, L):
     """One tensor-parallel shard (attention width H * 128 < D): the shard's
