@@ -229,9 +229,9 @@ def _measured_hbm_gbps() -> float:
 
 
 def _copy_calibration(n_bytes: int = 256 << 20, launches: int = 3) -> None:
-    """Launch the plain copy kernel over a buffer of known size.  Under
-    `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE` its counter values are the
-    scale that turns the decoder kernels' counters into bytes."""
+    """Launch the plain (cached) copy kernel over a buffer of known size.
+    Under `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE` its counter values are
+    the scale that turns the other kernels' counters into bytes."""
     import torch
 
     from metalbench_amd import native
@@ -243,10 +243,10 @@ def _copy_calibration(n_bytes: int = 256 << 20, launches: int = 3) -> None:
     b = [native.make_binding(0, native.ROLE_INPUT, "f32", src.data_ptr(), n_bytes),
          native.make_binding(1, native.ROLE_OUTPUT, "f32", dst.data_ptr(), n_bytes),
          native.make_binding(2, native.ROLE_SCALAR, "u32", value=n)]
-    native.run(native.kernel_find("copy_f32"), b, 0, launches, native.RUN_PIPELINED)
+    native.run(native.kernel_find("copy_f32_plain"), b, 0, launches, native.RUN_PIPELINED)
     torch.cuda.synchronize()
-    print(f"[bench] copy calibration: {launches} x copy_f32 of {n_bytes} bytes", file=sys.stderr,
-          flush=True)
+    print(f"[bench] copy calibration: {launches} x copy_f32_plain of {n_bytes} bytes",
+          file=sys.stderr, flush=True)
 
 
 # HBM-bound workloads are timed cold: their working set (weights + KV cache,

@@ -9,7 +9,12 @@
 //    lane (same box);
 //  * the scale factor of the FETCH_SIZE / WRITE_SIZE counters: a copy of N
 //    bytes must read N and write N bytes of HBM, so counter / N calibrates
-//    counter readings taken on the other kernels.
+//    counter readings taken on the other kernels.  That is copy_f32_plain
+//    (cached loads and stores): the counters read the non-temporal copy at
+//    twice its bytes (FETCH 259,537 KiB and WRITE 519,144 KiB per 256 MiB,
+//    against 131,096 and 262,144 for the plain copy), while the other
+//    kernels follow the plain copy's scale -- the transpose, which also uses
+//    non-temporal accesses and moves a known 537 MB, reads 1.001x with it.
 #include "common.h"
 
 namespace mb {
@@ -35,13 +40,29 @@ void copy_f32_kernel(const f32x4v* __restrict__ src, f32x4v* __restrict__ dst, u
     }
 }
 
+__global__ __launch_bounds__(THREADS)
+void copy_f32_plain_kernel(const f32x4v* __restrict__ src, f32x4v* __restrict__ dst, uint64_t n4) {
+    const uint64_t base = ((uint64_t)blockIdx.x * THREADS * VEC_PER_THREAD) + threadIdx.x;
+    f32x4v v[VEC_PER_THREAD];
+#pragma unroll
+    for (int i = 0; i < VEC_PER_THREAD; ++i) {
+        const uint64_t j = base + (uint64_t)i * THREADS;
+        if (j < n4) v[i] = src[j];
+    }
+#pragma unroll
+    for (int i = 0; i < VEC_PER_THREAD; ++i) {
+        const uint64_t j = base + (uint64_t)i * THREADS;
+        if (j < n4) dst[j] = v[i];
+    }
+}
+
 __global__ void copy_f32_tail_kernel(const float* __restrict__ src, float* __restrict__ dst,
                                      uint64_t start, uint64_t n) {
     const uint64_t i = start + threadIdx.x;
     if (i < n) dst[i] = src[i];
 }
 
-int launch_copy(const float* src, float* dst, uint64_t n, hipStream_t s) {
+int launch_copy(const float* src, float* dst, uint64_t n, hipStream_t s, bool plain = false) {
     if (n == 0) return MB_OK;
     if (!src || !dst) return fail(MB_E_ARG, "copy_f32: null pointer");
     if (((uintptr_t)src | (uintptr_t)dst) & 15)
@@ -51,8 +72,9 @@ int launch_copy(const float* src, float* dst, uint64_t n, hipStream_t s) {
         const uint64_t per_block = (uint64_t)THREADS * VEC_PER_THREAD;
         const uint64_t blocks = (n4 + per_block - 1) / per_block;
         if (blocks > 0x7fffffffull) return fail(MB_E_ARG, "copy_f32: size too large");
-        hipLaunchKernelGGL(copy_f32_kernel, dim3((uint32_t)blocks), dim3(THREADS), 0, s,
-                           reinterpret_cast<const f32x4v*>(src), reinterpret_cast<f32x4v*>(dst), n4);
+        hipLaunchKernelGGL(plain ? copy_f32_plain_kernel : copy_f32_kernel, dim3((uint32_t)blocks),
+                           dim3(THREADS), 0, s, reinterpret_cast<const f32x4v*>(src),
+                           reinterpret_cast<f32x4v*>(dst), n4);
         MB_LAUNCH_CHECK("copy_f32");
     }
     if (n4 * 4 < n) {
@@ -72,8 +94,8 @@ void evict_kernel(uint4* __restrict__ buf, uint64_t n16, uint32_t stamp) {
         buf[i] = uint4{stamp, (uint32_t)i, (uint32_t)(i >> 32), stamp};
 }
 
-// Registry launcher: src@0 (input f32), dst@1 (output f32), n@2 (elements).
-int run_copy(const Bindings& bs, hipStream_t s, PartMarks*) {
+// Registry launchers: src@0 (input f32), dst@1 (output f32), n@2 (elements).
+int run_copy_impl(const Bindings& bs, hipStream_t s, bool plain) {
     uint32_t n;
     int rc;
     if ((rc = bs.u32(2, &n, "n"))) return rc;
@@ -81,7 +103,11 @@ int run_copy(const Bindings& bs, hipStream_t s, PartMarks*) {
     if ((rc = bs.buffer(0, MB_DTYPE_F32, (uint64_t)n * 4, false, &a, "src")) ||
         (rc = bs.buffer(1, MB_DTYPE_F32, (uint64_t)n * 4, true, &b, "dst")))
         return rc;
-    return launch_copy((const float*)a, (float*)b, n, s);
+    return launch_copy((const float*)a, (float*)b, n, s, plain);
+}
+int run_copy(const Bindings& bs, hipStream_t s, PartMarks*) { return run_copy_impl(bs, s, false); }
+int run_copy_plain(const Bindings& bs, hipStream_t s, PartMarks*) {
+    return run_copy_impl(bs, s, true);
 }
 
 }  // namespace
@@ -99,6 +125,8 @@ int launch_cache_eviction(hipStream_t s) {
 
 void register_copy() {
     register_kernel({"copy_f32", run_copy, reinterpret_cast<const void*>(&copy_f32_kernel), 1});
+    register_kernel({"copy_f32_plain", run_copy_plain,
+                     reinterpret_cast<const void*>(&copy_f32_plain_kernel), 1});
 }
 
 }  // namespace mb

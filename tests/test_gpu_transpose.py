@@ -101,3 +101,18 @@ def test_copy_bit_exact(mb, dev, n):
     d_b = torch.full((n,), float("nan"), device=dev)
     launch("mb_launch_copy_f32", ptr(d_a), ptr(d_b), n, None)
     assert np.array_equal(bits32(d_b), a.numpy().view(np.int32))
+
+
+@pytest.mark.parametrize("n", [1, 5, 4096 * 257 + 3])
+def test_plain_copy_bit_exact(mb, dev, n):
+    """copy_f32_plain (cached accesses: the FETCH_SIZE / WRITE_SIZE
+    calibration kernel) through mb_run: bit-exact, tail included."""
+    a = seeded(n + 7, (n,))
+    d_a = a.to(dev)
+    d_b = torch.full((n,), float("nan"), device=dev)
+    binds = [native.make_binding(0, native.ROLE_INPUT, "f32", ptr(d_a), 4 * n),
+             native.make_binding(1, native.ROLE_OUTPUT, "f32", ptr(d_b), 4 * n),
+             native.make_binding(2, native.ROLE_SCALAR, "u32", value=n)]
+    native.run(native.kernel_find("copy_f32_plain"), binds, 0, 1, native.RUN_SYNC_EACH)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits32(d_b), a.numpy().view(np.int32))
