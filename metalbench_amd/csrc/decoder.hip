@@ -132,6 +132,45 @@ __device__ __forceinline__ void* uniform_ptr(const void* ptr) {
     return reinterpret_cast<void*>((hi << 32) | lo);
 }
 
+// The first two K units of the next skinny GEMM's weights for one block
+// index (w = nullptr: none; also for weights of 4 GB or more, which 32-bit
+// buffer offsets do not reach).  Column tile t covers bytes [seg_bytes t,
+// +seg_bytes) of every weight row, and for the paired gate | up tile also
+// the same range seg2_off bytes further on.
+struct NextUnits {
+    const uint8_t* w;
+    uint32_t bytes, ldw_bytes, tiles, kc, k, ur, seg_bytes, seg2_off;
+};
+
+// A workgroup that is not the last of its tile has nothing left to do while
+// the last one sums the partials and runs the epilogue (1-3 us), and HBM is
+// idle meanwhile.  It touches every 128-byte line of the next GEMM's first
+// two units for its own block index: hardware block b runs on XCD b % 8 in
+// both kernels, so those lines are in that XCD's L2 when the next kernel's
+// block b issues its first loads (cached loads: they allocate in L2).  The
+// wave waits for them before it ends, as it would at s_endpgm anyway.
+// Measured at the BASELINE shape: 115.7-116.2 -> 113.3-113.9 us per step
+// (three units: the same; four: slower).
+__device__ __noinline__ void prefetch_next_units(const NextUnits c, uint32_t b) {
+    if (!c.w) return;
+    const uint32_t tile = b % c.tiles, split = b / c.tiles;
+    const uint32_t k0 = split * c.kc;
+    if (k0 >= c.k) return;
+    const uint32_t rows = min(2 * c.ur, min(c.kc, c.k - k0));
+    const uint32_t lps = c.seg_bytes / 128;            // lines per segment
+    const uint32_t lpr = lps * (c.seg2_off ? 2 : 1);   // lines per weight row
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(c.w), 0, c.bytes, RSRC_FLAGS);
+    uint32_t acc = 0;
+    for (uint32_t L = threadIdx.x; L < rows * lpr; L += blockDim.x) {
+        const uint32_t row = L / lpr, sg = L % lpr;
+        const uint32_t off = (k0 + row) * c.ldw_bytes + tile * c.seg_bytes +
+                             (sg / lps) * c.seg2_off + (sg % lps) * 128;
+        acc ^= __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    }
+    asm volatile("" ::"v"(acc));   // keep the loads
+}
+
 // Signal "my sc1 stores are done" and return true in the workgroup that
 // completes `target` arrivals on `counter` (which it resets for the next use).
 __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t target, uint32_t* s_flag) {
@@ -171,6 +210,7 @@ struct StepParams {
     float* sumsq2;             // [D / 128][16] sum of x1^2 per column tile
     uint16_t* act;             // [B][FF] bf16(silu(g) u)
     uint16_t* act_lo;          // [B][FF] its rounding remainder
+    NextUnits next[4];         // indexed by EPI: what the kernel before that GEMM prefetches
 };
 
 struct GemmCfg {
@@ -382,7 +422,10 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
     }
     // QKV: no finisher; each attention workgroup sums the partials it needs.
     if (EPI == EPI_QKV) return;
-    if (!arrive_last(&g.counters[tile], g.splits, &s_last)) return;
+    if (!arrive_last(&g.counters[tile], g.splits, &s_last)) {
+        if (EPI == EPI_WO || EPI == EPI_GU) prefetch_next_units(p.next[EPI + 1], blockIdx.x);
+        return;
+    }
 
     // ---- finisher: this workgroup is the last of its tile ----
     // One memory round trip: the first SB splits' partials and the epilogue's
@@ -844,7 +887,10 @@ void attention_kernel(StepParams p) {
             st_sc1(ars, part0 + (h * APITCH + DH + 1) * 4, L);
         }
     }
-    if (!arrive_last(&p.attn_counters[bk], p.nsplit, &s_last)) return;
+    if (!arrive_last(&p.attn_counters[bk], p.nsplit, &s_last)) {
+        prefetch_next_units(p.next[EPI_WO], blockIdx.x);
+        return;
+    }
 
     // ---- merge: the splits' partials plus the new token ----
     // One memory round trip in the common case: the first U splits' partials
@@ -1154,6 +1200,21 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
     const GemmCfg g_dn =
         gemm(EPI_DOWN, p.act, p.act_lo, FF, a->w_down, D, FF, pl.counter_base[3]);
 
+    auto next_units = [&](int e, const uint16_t* w, uint32_t ldw, uint32_t k, uint32_t seg2) {
+        NextUnits c;
+        const uint64_t bytes = (uint64_t)k * ldw * 2;
+        c.w = bytes <= 0xffffffffull ? reinterpret_cast<const uint8_t*>(w) : nullptr;
+        c.bytes = (uint32_t)std::min<uint64_t>(bytes, 0xffffffffull);
+        c.ldw_bytes = ldw * 2; c.tiles = pl.tiles[e]; c.kc = pl.kc[e]; c.k = k;
+        c.ur = KS / pl.ww[e];                                    // k rows per unit
+        c.seg_bytes = seg2 ? 128 * pl.ww[e] : 256 * pl.ww[e];   // (paired: each half)
+        c.seg2_off = seg2;
+        return c;
+    };
+    p.next[EPI_QKV] = NextUnits{};
+    p.next[EPI_WO] = next_units(EPI_WO, a->w_o, D, QD, 0);
+    p.next[EPI_GU] = next_units(EPI_GU, a->w_gu, 2 * FF, D, 2 * FF);
+    p.next[EPI_DOWN] = next_units(EPI_DOWN, a->w_down, D, FF, 0);
     auto mark = [&](const char* name) { if (pm) pm->mark(s, name); };
     mark("qkv");
     launch_skinny<EPI_QKV>(g_qkv, pl, p, s);
