@@ -145,12 +145,13 @@ struct NextUnits {
 // A workgroup that is not the last of its tile has nothing left to do while
 // the last one sums the partials and runs the epilogue (1-3 us), and HBM is
 // idle meanwhile.  It touches every 128-byte line of the next GEMM's first
-// two units for its own block index: hardware block b runs on XCD b % 8 in
-// both kernels, so those lines are in that XCD's L2 when the next kernel's
-// block b issues its first loads (cached loads: they allocate in L2).  The
-// wave waits for them before it ends, as it would at s_endpgm anyway.
-// Measured at the BASELINE shape: 115.7-116.2 -> 113.3-113.9 us per step
-// (three units: the same; four: slower).
+// two units for its own block index, so that the next kernel's first loads
+// find them in the 256 MB memory-side cache instead of HBM.  (Not in L2: L2
+// does not keep them across the kernel boundary -- the L2-miss counter
+// FETCH_SIZE counts those lines in both kernels.)  The wave waits for them
+// before it ends, as it would at s_endpgm anyway.  Measured at the BASELINE
+// shape: 115.7-116.2 -> 113.3-113.9 us per step (three units: the same;
+// four: slower).
 __device__ __noinline__ void prefetch_next_units(const NextUnits c, uint32_t b) {
     if (!c.w) return;
     const uint32_t tile = b % c.tiles, split = b / c.tiles;
