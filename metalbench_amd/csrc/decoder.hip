@@ -132,6 +132,27 @@ __device__ __forceinline__ void* uniform_ptr(const void* ptr) {
     return reinterpret_cast<void*>((hi << 32) | lo);
 }
 
+// K splits of a skinny GEMM.  Every column tile has `splits` splits of kc
+// rows, except the tiles of the slow class ((t & slow_mask) == slow_val),
+// which, when splits_slow = splits + 1, have splits_slow splits of kc_slow
+// rows.  Blocks 0 .. tiles * splits - 1 are (tile b % tiles, split b /
+// tiles); the blocks after them are the last split of each slow tile, in
+// tile order.  A tile's partials sit at stride() splits per tile.
+struct SplitGeom {
+    uint32_t tiles, splits, kc, splits_slow, kc_slow, slow_mask, slow_val;
+    __host__ __device__ uint32_t stride() const { return splits_slow > splits ? splits_slow : splits; }
+    __host__ __device__ bool slow(uint32_t t) const {
+        return splits_slow > splits && (t & slow_mask) == slow_val;
+    }
+    __host__ __device__ uint32_t nsplits(uint32_t t) const { return slow(t) ? splits_slow : splits; }
+    __host__ __device__ uint32_t kc_of(uint32_t t) const { return slow(t) ? kc_slow : kc; }
+    __host__ __device__ void block(uint32_t b, uint32_t* t, uint32_t* sp) const {
+        const uint32_t nbase = tiles * splits;
+        if (b < nbase) { *t = b % tiles; *sp = b / tiles; }
+        else { *t = (b - nbase) * (slow_mask + 1) + slow_val; *sp = splits; }
+    }
+};
+
 // The first two K units of the next skinny GEMM's weights for one block
 // index (w = nullptr: none; also for weights of 4 GB or more, which 32-bit
 // buffer offsets do not reach).  Column tile t covers bytes [seg_bytes t,
@@ -139,7 +160,8 @@ __device__ __forceinline__ void* uniform_ptr(const void* ptr) {
 // the same range seg2_off bytes further on.
 struct NextUnits {
     const uint8_t* w;
-    uint32_t bytes, ldw_bytes, tiles, kc, k, ur, seg_bytes, seg2_off;
+    uint32_t bytes, ldw_bytes, k, ur, seg_bytes, seg2_off;
+    SplitGeom sp;
 };
 
 // A workgroup that is not the last of its tile has nothing left to do while
@@ -154,10 +176,12 @@ struct NextUnits {
 // four: slower).
 __device__ __noinline__ void prefetch_next_units(const NextUnits c, uint32_t b) {
     if (!c.w) return;
-    const uint32_t tile = b % c.tiles, split = b / c.tiles;
-    const uint32_t k0 = split * c.kc;
+    uint32_t tile, split;
+    c.sp.block(b, &tile, &split);
+    if (tile >= c.sp.tiles) return;
+    const uint32_t kc = c.sp.kc_of(tile), k0 = split * kc;
     if (k0 >= c.k) return;
-    const uint32_t rows = min(2 * c.ur, min(c.kc, c.k - k0));
+    const uint32_t rows = min(2 * c.ur, min(kc, c.k - k0));
     const uint32_t lps = c.seg_bytes / 128;            // lines per segment
     const uint32_t lpr = lps * (c.seg2_off ? 2 : 1);   // lines per weight row
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
@@ -199,7 +223,7 @@ struct StepParams {
     float* partial;            // split-K partials [tiles * splits][16][tile columns]
     uint32_t partial_bytes;
     float* sumsq;              // [qkv splits][16] sum of x^2 over each split
-    uint32_t qkv_splits;       // K splits of the QKV GEMM (its partials' split count)
+    SplitGeom qkv_sp;          // K splits of the QKV GEMM (its partials' layout)
     float* rope;               // [Dh / 2][2] cos, sin of pair i at position cache_len
     float* attn_part;          // [B][Hkv][nsplit][G][DH + 4]  (o[DH], m, l, pad)
     uint32_t attn_part_bytes;
@@ -220,7 +244,8 @@ struct GemmCfg {
     uint32_t lda;
     const uint16_t* w;     // weights [k][ldw]
     uint32_t ldw;
-    uint32_t k, kc, splits, tiles;
+    uint32_t k;
+    SplitGeom sp;
     uint32_t paired;       // 1: tile t = gate cols [64t, 64t+64) + up cols ff + [64t, 64t+64)
     uint32_t* counters;    // [tiles]
 };
@@ -289,10 +314,11 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t cw = wave % WW, rw = wave / WW;       // wave's column slab, row slab
     const uint32_t kq = lane >> 4, nl = lane & 15;
-    const uint32_t tile = blockIdx.x % g.tiles;
-    const uint32_t split = blockIdx.x / g.tiles;
-    const uint32_t k_begin = split * g.kc;
-    const uint32_t k_rows = min(g.kc, g.k - k_begin);   // a multiple of 32
+    uint32_t tile, split;
+    g.sp.block(blockIdx.x, &tile, &split);
+    const uint32_t kc = g.sp.kc_of(tile), nsplit = g.sp.nsplits(tile);
+    const uint32_t k_begin = split * kc;
+    const uint32_t k_rows = min(kc, g.k - k_begin);   // a multiple of 32
 
     // ---- the ring ----
     const uint32_t a_bytes = __builtin_amdgcn_readfirstlane(p.batch * g.lda * 2);
@@ -344,7 +370,7 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
 #pragma unroll
     for (int c = 0; c < 8; ++c) acc[c] = f32x4{};
     float ss = 0.f;
-    const uint32_t trips = ((g.kc + UR - 1) / UR + R - 1) / R;
+    const uint32_t trips = ((kc + UR - 1) / UR + R - 1) / R;
 
     for (uint32_t t = 0; t < trips; ++t) {
 #pragma unroll
@@ -412,7 +438,7 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
     // split-K partial: the same row-major tile, float4 q at byte 16 q
     constexpr uint32_t SPLIT_BYTES = MROWS * TBN * 4;
     const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(p.partial, p.partial_bytes);
-    const uint32_t tile_base = tile * g.splits * SPLIT_BYTES;
+    const uint32_t tile_base = tile * g.sp.stride() * SPLIT_BYTES;
 #pragma unroll
     for (int h = 0; h < NQ; ++h) st_sc1(prs, tile_base + split * SPLIT_BYTES + (tid + 256 * h) * 16, v[h]);
     const __amdgpu_buffer_rsrc_t srs = coherent_rsrc(p.sumsq, p.sumsq_bytes);
@@ -423,7 +449,7 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
     }
     // QKV: no finisher; each attention workgroup sums the partials it needs.
     if (EPI == EPI_QKV) return;
-    if (!arrive_last(&g.counters[tile], g.splits, &s_last)) {
+    if (!arrive_last(&g.counters[tile], nsplit, &s_last)) {
         if (EPI == EPI_WO || EPI == EPI_GU) prefetch_next_units(p.next[EPI + 1], blockIdx.x);
         return;
     }
@@ -438,7 +464,7 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
     // finishes, so the result does not depend on arrival order.
     constexpr uint32_t SB = NQ >= 8 ? 4 : 8;   // splits per batch of partial loads
     const __amdgpu_buffer_rsrc_t trs = coherent_rsrc(
-        reinterpret_cast<const uint8_t*>(p.partial) + tile_base, g.splits * SPLIT_BYTES);
+        reinterpret_cast<const uint8_t*>(p.partial) + tile_base, nsplit * SPLIT_BYTES);
     const uint32_t row = tid & 15, grp = tid >> 4;   // row statistics: row, group of tiles
     f32x4 w[SB][NQ];
 #pragma unroll
@@ -471,7 +497,7 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
 #pragma unroll
             for (uint32_t u = 1; u < SB; ++u) sum[h] += w[u][h];
         }
-        for (uint32_t sp0 = SB; sp0 < g.splits; sp0 += SB) {   // more than SB splits
+        for (uint32_t sp0 = SB; sp0 < nsplit; sp0 += SB) {   // more than SB splits
 #pragma unroll
             for (uint32_t u = 0; u < SB; ++u)
 #pragma unroll
@@ -675,33 +701,37 @@ void attention_kernel(StepParams p) {
     // them; split 0 also writes k_new and v_new out.
     constexpr uint32_t SPLIT_BYTES = MROWS * DH * 4;
     constexpr uint32_t PB = 16;   // splits loaded ahead of the first K/V block
-    const uint32_t qsp = p.qkv_splits;
+    const SplitGeom& qg = p.qkv_sp;
+    const uint32_t qsp0 = qg.nsplits(0);   // tile 0 wrote the per-split sums of x^2
     const uint32_t nitems_q = (G + 2) * (DH / 4);           // (head, column quad) items
     const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
-        p.sumsq, 0, __builtin_amdgcn_readfirstlane(qsp * MROWS * 4), RSRC_FLAGS);
+        p.sumsq, 0, __builtin_amdgcn_readfirstlane(qsp0 * MROWS * 4), RSRC_FLAGS);
     const __amdgpu_buffer_rsrc_t prs =
         __builtin_amdgcn_make_buffer_rsrc(p.partial, 0, p.partial_bytes, RSRC_FLAGS);
+    // item -> (its tile's partials at split 0, the tile's split count)
+    auto item_tile = [&](uint32_t idx) -> uint32_t {
+        const uint32_t ts = idx / (DH / 4);
+        return ts < G ? kvh * G + ts : p.qd / DH + (ts - G) * p.hkv + kvh;
+    };
     auto item_base = [&](uint32_t idx) -> uint32_t {
-        const uint32_t ts = idx / (DH / 4), c = idx % (DH / 4);
-        const uint32_t tile = ts < G ? kvh * G + ts : p.qd / DH + (ts - G) * p.hkv + kvh;
-        return tile * qsp * SPLIT_BYTES + b * (DH * 4) + 16 * c;
+        return item_tile(idx) * qg.stride() * SPLIT_BYTES + b * (DH * 4) + 16 * (idx % (DH / 4));
     };
     f32x4 pw[PB];
-    auto load_item = [&](uint32_t base, uint32_t c0) {
+    auto load_item = [&](uint32_t base, uint32_t n, uint32_t c0) {
 #pragma unroll
         for (uint32_t u = 0; u < PB; ++u)
             pw[u] = __builtin_bit_cast(
                 f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                           prs, c0 + u < qsp ? base + (c0 + u) * SPLIT_BYTES : 0x80000000u, 0, 0));
+                           prs, c0 + u < n ? base + (c0 + u) * SPLIT_BYTES : 0x80000000u, 0, 0));
     };
     // The splits are summed left to right: sum = w0 + w1 + ... (loads past
     // the last split add zeros).
-    auto sum_item = [&](uint32_t base) -> f32x4 {
+    auto sum_item = [&](uint32_t base, uint32_t n) -> f32x4 {
         f32x4 sum = pw[0];
 #pragma unroll
         for (uint32_t u = 1; u < PB; ++u) sum += pw[u];
-        for (uint32_t c0 = PB; c0 < qsp; c0 += PB) {   // more splits: loads after the K/V block's
-            load_item(base, c0);
+        for (uint32_t c0 = PB; c0 < n; c0 += PB) {   // more splits: loads after the K/V block's
+            load_item(base, n, c0);
 #pragma unroll
             for (uint32_t u = 0; u < PB; ++u) sum += pw[u];
         }
@@ -721,9 +751,9 @@ void attention_kernel(StepParams p) {
     // (vmcnt retires loads in issue order: a wait for a later load would also
     // wait for that block and delay the next block's issue).
     const uint32_t item0 = min(tid, nitems_q - 1);
-    const uint32_t base0 = item_base(item0);
+    const uint32_t base0 = item_base(item0), n0 = qg.nsplits(item_tile(item0));
     load_xs(0);
-    load_item(base0, 0);
+    load_item(base0, n0, 0);
     const f32x4 rope0 = *reinterpret_cast<const f32x4*>(p.rope + 4 * (item0 % (DH / 4)));
     KVBlock kv[AR];
 #pragma unroll
@@ -736,7 +766,7 @@ void attention_kernel(StepParams p) {
         float sv = 0.f;
 #pragma unroll
         for (uint32_t u = 0; u < XB; ++u) sv += xs[u];
-        for (uint32_t t0 = 16 * XB; t0 < qsp; t0 += 16 * XB) {   // more than 128 splits
+        for (uint32_t t0 = 16 * XB; t0 < qsp0; t0 += 16 * XB) {   // more than 128 splits
             load_xs(t0);
 #pragma unroll
             for (uint32_t u = 0; u < XB; ++u) sv += xs[u];
@@ -769,11 +799,13 @@ void attention_kernel(StepParams p) {
                 *reinterpret_cast<uint2*>((ts == G ? p.k_new : p.v_new) + (size_t)bk * DH + 4 * c) = out;
         }
     };
-    if (tid < nitems_q) finish_item(tid, sum_item(base0), rope0);
+    if (tid < nitems_q) finish_item(tid, sum_item(base0, n0), rope0);
     for (uint32_t idx = tid + 256; idx < nitems_q; idx += 256) {   // G > 4: more items
         const uint32_t base = item_base(idx);
-        load_item(base, 0);
-        finish_item(idx, sum_item(base), *reinterpret_cast<const f32x4*>(p.rope + 4 * (idx % (DH / 4))));
+        const uint32_t n = qg.nsplits(item_tile(idx));
+        load_item(base, n, 0);
+        finish_item(idx, sum_item(base, n),
+                    *reinterpret_cast<const f32x4*>(p.rope + 4 * (idx % (DH / 4))));
     }
     {   // query rows past G are zero
         const uint32_t qh = tid / (DH / 8), qc = tid % (DH / 8);
@@ -973,6 +1005,7 @@ void attention_kernel(StepParams p) {
 struct Plan {
     uint32_t nqkv, g, nsplit, split_keys;
     uint32_t tiles[4], splits[4], kc[4], ring[4], ww[4];
+    SplitGeom geo[4];
     size_t off_counters, off_partial, off_sumsq, off_rope, off_attn_part, off_attn_out, off_x1,
         off_x1b, off_x1b_lo, off_sumsq2, off_act, off_act_lo, total;
     uint32_t counter_base[4];   // attn, wo, gu, down (the QKV GEMM has no finisher)
@@ -1011,6 +1044,43 @@ static void choose_split(uint32_t tiles, uint32_t k, uint32_t ww, uint32_t* spli
     *kc = per * KG;
     const uint32_t units = cdiv(*kc, KS / ww);
     *ring = units >= RING ? RING : (units >= 2 ? 2 : 1);
+}
+
+// Column tiles of the slow address class get one split more (fewer rows
+// each) when the grid has room for them.  With the weights 1 KB aligned (as
+// hipMalloc'd buffers are) and a row pitch that is a multiple of 1 KB, a
+// 128-column tile t reads the 256-byte pieces of address class t % 4 in every
+// row, and the workgroups of class 1 stream ~11-18 % slower than the others
+// (measured per tile: QKV 8.9 against 7.7 us, down 19.1 against 16.2 us); a
+// 512-column gate | up tile holds class 1 when t is even (34.4 against
+// 31.0 us).  The classes are taken from the tile index alone, so the split
+// layout -- and every output bit -- does not depend on where the weights
+// are; weights at another alignment only lose the balance.
+static void plan_slow_class(Plan* pl, int e, uint32_t k, uint32_t ldw, bool paired,
+                            uint32_t up_offset_bytes) {
+    SplitGeom& g = pl->geo[e];
+    g.tiles = pl->tiles[e]; g.splits = pl->splits[e]; g.kc = pl->kc[e];
+    g.splits_slow = g.splits; g.kc_slow = g.kc; g.slow_mask = 0; g.slow_val = 1;
+    if ((ldw * 2) % 1024 || up_offset_bytes % 1024) return;
+    if (!paired && pl->ww[e] == 1) { g.slow_mask = 3; g.slow_val = 1; }
+    else if (paired && pl->ww[e] == 4) { g.slow_mask = 1; g.slow_val = 0; }
+    else return;
+    uint32_t n_slow = 0;
+    for (uint32_t t = 0; t < g.tiles; ++t) n_slow += (t & g.slow_mask) == g.slow_val;
+    const uint32_t groups = k / KG;
+    const uint32_t per = cdiv(groups, g.splits + 1);
+    if (n_slow == 0 || g.tiles * g.splits + n_slow > PLAN_CUS || per * KG < MIN_KC ||
+        cdiv(groups, per) != g.splits + 1)
+        return;
+    g.splits_slow = g.splits + 1;
+    g.kc_slow = per * KG;
+}
+
+static uint32_t grid_blocks(const SplitGeom& g) {
+    uint32_t n = g.tiles * g.splits;
+    if (g.splits_slow > g.splits)
+        for (uint32_t t = 0; t < g.tiles; ++t) n += (t & g.slow_mask) == g.slow_val;
+    return n;
 }
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -1081,10 +1151,11 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
         if ((trips + 1) * pl->ring[i] * unit * ldw[i] * 2 > 0xffffffffull ||
             (uint64_t)B * k * 2 >= 0x80000000ull)
             return fail(MB_E_ARG, "decoder step: shapes too large for 32-bit weight offsets");
+        plan_slow_class(pl, i, k, ldw[i], i == EPI_GU, i == EPI_GU ? 2 * FF : 0);
     }
     size_t max_part = 0;
     for (int i = 0; i < 4; ++i)
-        max_part = std::max(max_part, (size_t)pl->tiles[i] * pl->splits[i] * pl->ww[i]);
+        max_part = std::max(max_part, (size_t)pl->tiles[i] * pl->geo[i].stride() * pl->ww[i]);
     const uint32_t n_counters =
         B * a->n_kv_heads + pl->tiles[EPI_WO] + pl->tiles[EPI_GU] + pl->tiles[EPI_DOWN];
     pl->counter_base[0] = 0;
@@ -1094,7 +1165,7 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
     size_t o = 0;
     pl->off_counters = o; o = align256(o + (size_t)n_counters * 4);
     pl->off_partial = o; o = align256(o + max_part * MROWS * BN * 4);
-    pl->off_sumsq = o; o = align256(o + (size_t)pl->splits[EPI_QKV] * MROWS * 4);
+    pl->off_sumsq = o; o = align256(o + (size_t)pl->geo[EPI_QKV].stride() * MROWS * 4);
     pl->off_rope = o; o = align256(o + DH / 2 * 2 * 4);
     pl->off_attn_part = o;
     o = align256(o + (size_t)B * a->n_kv_heads * pl->nsplit * pl->g * APITCH * 4);
@@ -1118,7 +1189,7 @@ static size_t counters_bytes(const Plan& pl) { return pl.off_partial; }
 
 template <int EPI, int WW>
 void launch_skinny_ww(const GemmCfg& g, uint32_t ring, const StepParams& p, hipStream_t s) {
-    const dim3 grid(g.tiles * g.splits), block(256);
+    const dim3 grid(grid_blocks(g.sp)), block(256);
     switch (ring) {
         case 1: hipLaunchKernelGGL((skinny_gemm_kernel<EPI, WW, 1>), grid, block, 0, s, g, p); break;
         case 2: hipLaunchKernelGGL((skinny_gemm_kernel<EPI, WW, 2>), grid, block, 0, s, g, p); break;
@@ -1172,7 +1243,7 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
     p.attn_part_bytes = (uint32_t)(pl.off_attn_out - pl.off_attn_part);
     p.sumsq = reinterpret_cast<float*>(ws + pl.off_sumsq);
     p.rope = reinterpret_cast<float*>(ws + pl.off_rope);
-    p.qkv_splits = pl.splits[EPI_QKV];
+    p.qkv_sp = pl.geo[EPI_QKV];
     p.attn_part = reinterpret_cast<float*>(ws + pl.off_attn_part);
     p.attn_out = reinterpret_cast<uint16_t*>(ws + pl.off_attn_out);
     p.x1 = reinterpret_cast<float*>(ws + pl.off_x1);
@@ -1187,7 +1258,7 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
                     const uint16_t* w, uint32_t ldw, uint32_t k, uint32_t counter_base) -> GemmCfg {
         GemmCfg g;
         g.a = act; g.a_lo = act_lo; g.lda = lda; g.w = w; g.ldw = ldw; g.k = k;
-        g.tiles = pl.tiles[epi]; g.splits = pl.splits[epi]; g.kc = pl.kc[epi];
+        g.sp = pl.geo[epi];
         g.paired = epi == EPI_GU ? 1u : 0u;
         g.counters = counters + counter_base;
         return g;
@@ -1206,7 +1277,7 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
         const uint64_t bytes = (uint64_t)k * ldw * 2;
         c.w = bytes <= 0xffffffffull ? reinterpret_cast<const uint8_t*>(w) : nullptr;
         c.bytes = (uint32_t)std::min<uint64_t>(bytes, 0xffffffffull);
-        c.ldw_bytes = ldw * 2; c.tiles = pl.tiles[e]; c.kc = pl.kc[e]; c.k = k;
+        c.ldw_bytes = ldw * 2; c.sp = pl.geo[e]; c.k = k;
         c.ur = KS / pl.ww[e];                                    // k rows per unit
         c.seg_bytes = seg2 ? 128 * pl.ww[e] : 256 * pl.ww[e];   // (paired: each half)
         c.seg2_off = seg2;

@@ -85,6 +85,7 @@ def _check(got, want, what):
     (7, 1024, 8, 2, 1024, 300),    # several 64-key blocks, ragged
     (16, 2048, 16, 4, 1536, 1000),  # GQA 4 as the full config, several splits
     (9, 2048, 16, 1, 1024, 77),    # G = 16
+    (4, 4096, 16, 4, 2048, 64),    # QKV tiles of the slow address class take 11 K splits, others 10
 ])
 def test_decoder_step_shapes(mb, dev, B, D, H, HKV, FF, L):
     ins = _make(B, D, H, HKV, FF, L)
