@@ -1367,7 +1367,7 @@ int run_decoder(const Bindings& bs, hipStream_t s, PartMarks* pm) {
 // with a fill kernel (a kernel, not hipMemsetAsync, so that graph capture
 // records a plain kernel node).  Every call on a device shares its scratch:
 // calls that overlap on one device race.
-constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)32 << 20;   // 32 MiB (9.6 MB at the BASELINE shape)
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)32 << 20;   // 32 MiB (11.3 MB at the BASELINE shape)
 static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
 static_assert(NOALLOC_SCRATCH_BYTES == MB_DECODER_NOALLOC_MAX_BYTES, "mbhip.h states the limit");
 
