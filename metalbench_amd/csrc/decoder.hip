@@ -171,7 +171,7 @@ struct NextUnits {
 // find them in the 256 MB memory-side cache instead of HBM.  (Not in L2: L2
 // does not keep them across the kernel boundary -- the L2-miss counter
 // FETCH_SIZE counts those lines in both kernels.)  The wave waits for them
-// before it ends, as it would at s_endpgm anyway.  Measured at the BASELINE
+// before it ends, as it would at s_endpgm anyway.  Measured at the benchmark
 // shape: 115.7-116.2 -> 113.3-113.9 us per step (three units: the same;
 // four: slower).
 __device__ __noinline__ void prefetch_next_units(const NextUnits c, uint32_t b) {
@@ -877,7 +877,7 @@ void attention_kernel(StepParams p) {
 
     // A ring of AR blocks: block t + AR - 1 is issued right before block t is
     // computed, so AR blocks (AR x 32 KB per workgroup) are in flight.  Four
-    // in flight measured 1.5 us slower than two at the BASELINE shape (more
+    // in flight measured 1.5 us slower than two at the benchmark shape (more
     // concurrent streams per CU, less DRAM page locality).  sched_barrier
     // pins the order.
     for (uint32_t t = 0; t < nblk; t += AR) {
@@ -1367,7 +1367,7 @@ int run_decoder(const Bindings& bs, hipStream_t s, PartMarks* pm) {
 // with a fill kernel (a kernel, not hipMemsetAsync, so that graph capture
 // records a plain kernel node).  Every call on a device shares its scratch:
 // calls that overlap on one device race.
-constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)32 << 20;   // 32 MiB (11.3 MB at the BASELINE shape)
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)32 << 20;   // 32 MiB (11.3 MB at the benchmark shape)
 static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
 static_assert(NOALLOC_SCRATCH_BYTES == MB_DECODER_NOALLOC_MAX_BYTES, "mbhip.h states the limit");
 

@@ -1,6 +1,6 @@
 """conv2d implicit GEMM (fp32 MFMA) on the GPU vs the float64 oracle.
 
-Gate: rtol 1e-3 (BASELINE) with the registry's atol 1e-3."""
+Gate: rtol 1e-3 (benchmark configuration) with the registry's atol 1e-3."""
 import numpy as np
 import pytest
 import torch

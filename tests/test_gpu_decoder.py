@@ -1,6 +1,6 @@
 """LLaMA decoder decode step on the GPU vs the float64 oracle.
 
-Gate (BASELINE): rtol 2e-2 with atol 2e-2 (outputs are O(1)), on y, k_new and
+Gate (benchmark configuration): rtol 2e-2 with atol 2e-2 (outputs are O(1)), on y, k_new and
 v_new.  Covers batch 1..16, empty / short / chunk-boundary caches, GQA group
 sizes 1..8, a padded cache stride, the caller-workspace path, repeat calls
 (self-resetting split-K counters must give bit-identical results) and the full
@@ -159,7 +159,7 @@ def test_decoder_step_rejects_bad_shapes(mb, dev):
 
 
 def test_decoder_step_registry_config(mb):
-    """Full BASELINE config: B 16, D 4096, 32/8 heads, FF 14336, L 2048."""
+    """Full benchmark config: B 16, D 4096, 32/8 heads, FF 14336, L 2048."""
     b, inputs, outs, k_t = run_registry("llama_decoder_step", seed=0, warmup=1, iters=3)
     f = oracle.as_f64
     want = oracle.llama_decoder_step(*[f(t) for t in inputs], n_heads=32, n_kv_heads=8)

@@ -1,6 +1,6 @@
 """bf16 GEMM (fp32 accumulate, bf16 out) on the GPU vs the float64 oracle.
 
-Gate (BASELINE): rtol 1e-2 against the fp32-accumulated product, atol 1e-4.
+Gate (benchmark configuration): rtol 1e-2 against the fp32-accumulated product, atol 1e-4.
 Stronger check: with fp32 accumulation the error before rounding is ~1e-6
 relative, far below half a bf16 ulp, so wherever |C| is not tiny (above 1% of
 its RMS, where a bf16 ulp still dwarfs the fp32 accumulation noise) the

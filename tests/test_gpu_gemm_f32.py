@@ -1,6 +1,6 @@
 """fp32 MFMA GEMM (sqr_mm / rect_mm) on the GPU vs the float64 oracle.
 
-Tolerance: rtol = atol = 1e-4 for the sqr_mm config (BASELINE), scaled with
+Tolerance: rtol = atol = 1e-4 for the sqr_mm benchmark config, scaled with
 sqrt(K) for the normal(0,1) shapes where |C| grows with K."""
 import numpy as np
 import pytest
