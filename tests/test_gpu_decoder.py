@@ -2,9 +2,10 @@
 
 Gate (benchmark configuration): rtol 2e-2 with atol 2e-2 (outputs are O(1)), on y, k_new and
 v_new.  Covers batch 1..16, empty / short / chunk-boundary caches, GQA group
-sizes 1..8, a padded cache stride, the caller-workspace path, repeat calls
-(self-resetting split-K counters must give bit-identical results) and the full
-registry configuration."""
+sizes 1..16, padded cache strides, tensor-parallel shards, shapes whose QKV
+tiles take class-dependent K splits, a seeded sweep of random shapes, the
+caller-workspace path, repeat calls (self-resetting split-K counters must give
+bit-identical results) and the full registry configuration."""
 import ctypes
 
 import numpy as np
@@ -104,6 +105,37 @@ def test_decoder_step_tensor_parallel_shard(mb, dev, B, D, H, HKV, FF, L):
     QKV columns, W_o rows and FFN slice, all-reduces left to the caller."""
     ins = _make(B, D, H, HKV, FF, L)
     _check(_run(dev, ins, B, D, H, HKV, FF, L), _want(ins, H, HKV, L), f"shard {B,D,H,HKV,FF,L}")
+
+
+def _random_shapes(n, seed=20261202):
+    """Seeded decode-step shapes inside the kernel's limits: batch 1..16,
+    d_model a multiple of 128, query heads a multiple of kv heads (G <= 16,
+    the attention width below or equal to d_model), d_ff a multiple of 128,
+    cache 0..700 keys with an optional padded stride."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        B = int(rng.integers(1, 17))
+        D = 128 * int(rng.integers(2, 25))            # 256 .. 3072
+        HKV = int(rng.choice([1, 2, 4, 8]))
+        G = int(rng.choice([1, 2, 4, 8, 16]))
+        H = HKV * G
+        if H * 128 > D:
+            continue
+        FF = 128 * int(rng.integers(1, 25))           # 128 .. 3072
+        L = int(rng.integers(0, 701))
+        S = L + int(rng.choice([0, 0, 1, 37]))
+        out.append((B, D, H, HKV, FF, L, S))
+    return out
+
+
+@pytest.mark.parametrize("B,D,H,HKV,FF,L,S", _random_shapes(10))
+def test_decoder_step_random_shapes(mb, dev, B, D, H, HKV, FF, L, S):
+    """A seeded sweep over the plan's shape space (split counts, ring depth,
+    attention splits, shard widths, strides) against the oracle."""
+    ins = _make(B, D, H, HKV, FF, L, stride=max(S, 1), seed=B + D + L)
+    _check(_run(dev, ins, B, D, H, HKV, FF, L, stride=max(S, 1)), _want(ins, H, HKV, L),
+           f"random {B,D,H,HKV,FF,L,S}")
 
 
 def test_decoder_step_new_inputs_every_call(mb, dev):
