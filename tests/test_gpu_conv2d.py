@@ -34,6 +34,28 @@ def test_conv2d_shapes(mb, dev, n, h, w, c, o, r, s, st, pad):
     assert_close(d_y.cpu().numpy(), want, 1e-3, 1e-3, f"conv2d {n,h,w,c,o,r,s,st,pad}")
 
 
+def _random_conv_shapes(n, seed=73):
+    """Seeded geometries: channel counts of the fast path (multiples of 32) and
+    of the generic one, 1x1 to 5x5 filters, stride 1 or 2, padding 0..2."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        r, s_ = int(rng.choice([1, 3, 5])), int(rng.choice([1, 3, 5]))
+        st, pad = int(rng.choice([1, 2])), int(rng.integers(0, 3))
+        nb, h, w = int(rng.integers(1, 4)), int(rng.integers(1, 17)), int(rng.integers(1, 17))
+        c = int(rng.choice([32, 64, 96, 5, 20]))
+        o = int(rng.integers(1, 140))
+        if h + 2 * pad < r or w + 2 * pad < s_:
+            continue
+        out.append((nb, h, w, c, o, r, s_, st, pad))
+    return out
+
+
+@pytest.mark.parametrize("n,h,w,c,o,r,s,st,pad", _random_conv_shapes(10))
+def test_conv2d_random_shapes(mb, dev, n, h, w, c, o, r, s, st, pad):
+    test_conv2d_shapes(mb, dev, n, h, w, c, o, r, s, st, pad)
+
+
 def test_conv2d_rejects_bad_geometry(mb, dev):
     from metalbench_amd import native
     lib = native.load()

@@ -50,6 +50,25 @@ def test_matmul_bf16_shapes(mb, dev, m, n, k):
     _check_rounding(_bits(d_c), exact, f"matmul_bf16 {m}x{n}x{k}")
 
 
+def _random_bf16_shapes(n, seed=71):
+    """Seeded shapes: half ragged (guarded and element-wise kernels), half full
+    256 x 256 tiles with K a multiple of 128 (the DMA kernel)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        if i % 2:
+            out.append((256 * int(rng.integers(1, 4)), 256 * int(rng.integers(1, 4)),
+                        128 * int(rng.integers(1, 7))))
+        else:
+            out.append(tuple(int(v) for v in rng.integers(1, 700, size=3)))
+    return out
+
+
+@pytest.mark.parametrize("m,n,k", _random_bf16_shapes(8))
+def test_matmul_bf16_random_shapes(mb, dev, m, n, k):
+    test_matmul_bf16_shapes(mb, dev, m, n, k)
+
+
 def test_matmul_bf16_identity_exact(mb, dev):
     a = seeded(11, (256, 512), ("normal", 0.0, 1.0), "bf16")
     eye = torch.eye(512, dtype=torch.bfloat16)

@@ -29,6 +29,25 @@ def test_matmul_f32_shapes(mb, dev, m, n, k):
     assert_close(d_c.cpu().numpy(), want, 1e-4, 1e-4, f"matmul_f32 {m}x{n}x{k}")
 
 
+def _random_f32_shapes(n, seed=72):
+    """Seeded shapes: half ragged, half full 64 x 64 tiles with K a multiple of
+    256 from 512 (the LDS-DMA kernel)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        if i % 2:
+            out.append((64 * int(rng.integers(1, 9)), 64 * int(rng.integers(1, 9)),
+                        256 * int(rng.integers(2, 5))))
+        else:
+            out.append(tuple(int(v) for v in rng.integers(1, 600, size=3)))
+    return out
+
+
+@pytest.mark.parametrize("m,n,k", _random_f32_shapes(8))
+def test_matmul_f32_random_shapes(mb, dev, m, n, k):
+    test_matmul_f32_shapes(mb, dev, m, n, k)
+
+
 def test_matmul_f32_k0_gives_zeros(mb, dev):
     d_c = torch.full((8, 8), 5.0, device=dev)
     d_a = torch.zeros(1, device=dev)

@@ -25,6 +25,12 @@ def test_transpose_bit_exact(mb, dev, rows, cols):
     assert np.array_equal(bits32(d_b), want.view(np.int32))
 
 
+@pytest.mark.parametrize("rows,cols", [tuple(int(v) for v in np.random.default_rng(74 + i)
+                                                 .integers(1, 2500, size=2)) for i in range(8)])
+def test_transpose_random_shapes_bit_exact(mb, dev, rows, cols):
+    test_transpose_bit_exact(mb, dev, rows, cols)
+
+
 def test_transpose_empty_is_noop(mb, dev):
     d_b = torch.full((4,), 3.0, device=dev)
     launch("mb_launch_transpose_2d_f32", ptr(d_b), ptr(d_b), 0, 4, None)
