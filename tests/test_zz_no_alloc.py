@@ -4,7 +4,8 @@ mb_launch_llama_decoder_step_bf16_noalloc runs the same kernels on a static
 device scratch; it must give bit-identical y, k_new and v_new to
 mb_launch_llama_decoder_step_bf16 (the decoder's own parity tests tie that
 entry point to the float64 oracle), on two calls in a row with the second one
-smaller, and reject shapes beyond its scratch size without touching the GPU."""
+smaller, replay from a captured HIP graph, and reject shapes beyond its
+scratch size without touching the GPU."""
 import ctypes
 
 import pytest
@@ -59,6 +60,33 @@ def test_noalloc_matches_allocating_entry_point(mb, dev):
         for g, w, name in zip(got, outs, ("y", "k_new", "v_new")):
             assert not torch.isnan(g.float()).any(), f"{cfg} {name}: not written"
             assert torch.equal(g, w), f"{cfg} {name}: no-alloc result differs"
+
+
+def test_noalloc_step_replays_from_a_captured_graph(mb, dev):
+    """The entry point's purpose: a caller that captures the step in a HIP
+    graph.  One eager call (which also clears the scratch counters), then a
+    capture, then three replays with eager work and synchronisation between
+    them; every replay must reproduce the eager outputs bit for bit."""
+    print("[no-alloc] graph capture and replays", flush=True)
+    lib = native.load()
+    a, d, outs = _args(dev, (4, 512, 4, 2, 512, 70), 7)
+    _call("mb_launch_llama_decoder_step_bf16_noalloc", a)
+    want = [t.clone() for t in outs]
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=stream):
+        rc = lib.mb_launch_llama_decoder_step_bf16_noalloc(
+            ctypes.byref(a), ctypes.c_void_p(stream.cuda_stream))
+    assert rc == 0, native.last_error()
+    for rep in range(3):
+        for t in outs:
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for g, w, name in zip(outs, want, ("y", "k_new", "v_new")):
+            assert torch.equal(g, w), f"replay {rep} {name}: differs from the eager call"
 
 
 def test_noalloc_rejects_oversized_shapes_and_a_workspace(mb, dev):
