@@ -262,10 +262,9 @@ typedef struct mb_decoder_step_args {
 
 /* Workspace bytes mb_launch_llama_decoder_step_bf16 needs for these shapes
  * (0 and mb_last_error() set if the shapes are unsupported).  A caller-owned
- * workspace must be zero-filled before its first use and again whenever the
- * shapes change; between calls with the same shapes the kernels leave it ready
- * (their completion counters return to zero).  Calls sharing one workspace
- * must not overlap.  Callable without a GPU. */
+ * workspace needs no initialisation: each step's first kernel clears the
+ * completion counters the others use.  Calls sharing one workspace must not
+ * overlap.  Callable without a GPU. */
 uint64_t mb_decoder_step_workspace_bytes(const mb_decoder_step_args* args);
 
 /* Enqueue one decode step.  `args->workspace` may be NULL: the library then
@@ -282,7 +281,9 @@ int mb_launch_llama_decoder_step_bf16(const mb_decoder_step_args* args, void* st
  * rejected with MB_E_ARG.  Results are bit-identical to
  * mb_launch_llama_decoder_step_bf16.  Every call on a device shares that
  * device's scratch and a call leaves its intermediates there: calls that
- * overlap on one device (two streams, two threads) race. */
+ * overlap on one device (two streams, two threads) race.  A HIP graph that
+ * captured a call may be replayed after calls of other shapes: each step
+ * clears its own completion counters. */
 #define MB_DECODER_NOALLOC_MAX_BYTES (32u << 20)
 int mb_launch_llama_decoder_step_bf16_noalloc(const mb_decoder_step_args* args, void* stream);
 

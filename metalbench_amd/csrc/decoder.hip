@@ -219,6 +219,8 @@ struct StepParams {
     float rope_base, eps;
     const uint16_t *x, *k_cache, *v_cache;
     uint16_t *y, *k_new, *v_new;
+    uint32_t* counters;        // every tile counter of the step (attention, W_o, gate/up, down)
+    uint32_t n_counters;
     uint32_t* attn_counters;   // [B * Hkv]
     float* partial;            // split-K partials [tiles * splits][16][tile columns]
     uint32_t partial_bytes;
@@ -357,6 +359,15 @@ void skinny_gemm_kernel(GemmCfg g, StepParams p) {
     // its first loads are in flight.  The angle pos * base^(-2i/Dh) is formed
     // and reduced mod 2 pi in fp64: an fp32 angle would be off by
     // ~pos * 6e-8 rad (0.06 rad at pos 10^6).
+    // QKV: workgroup 0 also clears every counter the step's later kernels
+    // count arrivals on.  Those kernels run after this one, so each step
+    // starts from zeroed counters whatever the workspace held: a caller's
+    // fresh workspace, or the no-alloc scratch after a call of other shapes
+    // (which a replayed HIP graph cannot check for).  The finishers also reset
+    // their counters when done.
+    if (EPI == EPI_QKV && blockIdx.x == 0)
+        for (uint32_t i = tid; i < p.n_counters; i += 256)
+            __hip_atomic_store(&p.counters[i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (EPI == EPI_QKV && blockIdx.x == 0 && tid < DH / 2) {
         const double omega = pow((double)p.rope_base, -2.0 * (double)tid / (double)DH);
         const double ang = (double)p.cache_len * omega;
@@ -1009,6 +1020,7 @@ struct Plan {
     size_t off_counters, off_partial, off_sumsq, off_rope, off_attn_part, off_attn_out, off_x1,
         off_x1b, off_x1b_lo, off_sumsq2, off_act, off_act_lo, total;
     uint32_t counter_base[4];   // attn, wo, gu, down (the QKV GEMM has no finisher)
+    uint32_t n_counters;
 };
 
 // K split of a skinny GEMM: enough splits that tiles x splits gives about one
@@ -1158,6 +1170,7 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
         max_part = std::max(max_part, (size_t)pl->tiles[i] * pl->geo[i].stride() * pl->ww[i]);
     const uint32_t n_counters =
         B * a->n_kv_heads + pl->tiles[EPI_WO] + pl->tiles[EPI_GU] + pl->tiles[EPI_DOWN];
+    pl->n_counters = n_counters;
     pl->counter_base[0] = 0;
     pl->counter_base[1] = pl->counter_base[0] + B * a->n_kv_heads;
     pl->counter_base[2] = pl->counter_base[1] + pl->tiles[EPI_WO];
@@ -1183,9 +1196,6 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
     return MB_OK;
 }
 
-// Only the counters must start at zero; every other region is written before
-// it is read within a step.
-static size_t counters_bytes(const Plan& pl) { return pl.off_partial; }
 
 template <int EPI, int WW>
 void launch_skinny_ww(const GemmCfg& g, uint32_t ring, const StepParams& p, hipStream_t s) {
@@ -1224,7 +1234,7 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
             return fail(MB_E_ARG, "decoder step: workspace %llu bytes, need %zu",
                         (unsigned long long)a->workspace_bytes, pl.total);
     } else {
-        ws = static_cast<uint8_t*>(library_workspace(pl.total, counters_bytes(pl), s));
+        ws = static_cast<uint8_t*>(library_workspace(pl.total, 0, s));
         if (!ws) return MB_E_HIP;
     }
 
@@ -1236,6 +1246,8 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
     p.x = a->x; p.k_cache = a->k_cache; p.v_cache = a->v_cache;
     p.y = a->y; p.k_new = a->k_new; p.v_new = a->v_new;
     uint32_t* counters = reinterpret_cast<uint32_t*>(ws + pl.off_counters);
+    p.counters = counters;
+    p.n_counters = pl.n_counters;
     p.attn_counters = counters + pl.counter_base[0];
     p.partial = reinterpret_cast<float*>(ws + pl.off_partial);
     p.partial_bytes = (uint32_t)(pl.off_sumsq - pl.off_partial);
@@ -1360,13 +1372,11 @@ int run_decoder(const Bindings& bs, hipStream_t s, PartMarks* pm) {
 // copy of the array for the life of the process; host code uses the device
 // address hipGetSymbolAddress returns for it (kept per device in
 // g_scratch), never the array's name, which in host code is only a
-// host-side stand-in.  Only the completion counters at the front of the
-// workspace must start at zero, and the kernels leave them at zero; a call
-// whose counters reach past what is known to be zero (the first call on a
-// device, or a shape with more counters than any before) clears them first
-// with a fill kernel (a kernel, not hipMemsetAsync, so that graph capture
-// records a plain kernel node).  Every call on a device shares its scratch:
-// calls that overlap on one device race.
+// host-side stand-in.  Nothing needs clearing before a call: the step's
+// first kernel zeroes the completion counters the later ones use, so a call
+// -- or a replay of a HIP graph that captured one -- is correct whatever an
+// earlier call of other shapes left in the scratch.  Every call on a device
+// shares its scratch: calls that overlap on one device race.
 constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)32 << 20;   // 32 MiB (11.3 MB at the benchmark shape)
 static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
 static_assert(NOALLOC_SCRATCH_BYTES == MB_DECODER_NOALLOC_MAX_BYTES, "mbhip.h states the limit");
@@ -1374,14 +1384,9 @@ static_assert(NOALLOC_SCRATCH_BYTES == MB_DECODER_NOALLOC_MAX_BYTES, "mbhip.h st
 constexpr int MAX_DEVICES = 64;
 struct DeviceScratch {
     void* ptr = nullptr;     // device address of `scratch` on that device
-    size_t zeroed = 0;       // leading bytes known to be zero
 };
 DeviceScratch g_scratch[MAX_DEVICES];
 std::mutex g_scratch_mutex;
-
-__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* __restrict__ p, uint32_t n) {
-    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0u;
-}
 
 // Looks up the scratch of the current device (once per device, with that
 // device current).
@@ -1399,7 +1404,6 @@ int scratch_of_current_device(DeviceScratch** out) {
             return fail(MB_E_HIP, "hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
                         hipGetErrorString(e));
         d.ptr = ptr;
-        d.zeroed = 0;
     }
     *out = &d;
     return MB_OK;
@@ -1417,15 +1421,8 @@ int launch_decoder_noalloc(const mb_decoder_step_args* a, hipStream_t s) {
                               "the static scratch holds %zu", pl.total, NOALLOC_SCRATCH_BYTES);
     DeviceScratch* d = nullptr;
     if ((rc = scratch_of_current_device(&d))) return rc;
-    const size_t zero = counters_bytes(pl);
-    if (zero > d->zeroed) {
-        const uint32_t words = (uint32_t)(zero / 4);   // counters_bytes is 256-byte aligned
-        hipLaunchKernelGGL(zero_words_kernel, dim3(std::min(cdiv(words, 256u), 1024u)), dim3(256),
-                           0, s, static_cast<uint32_t*>(d->ptr), words);
-        MB_LAUNCH_CHECK("decoder scratch clear");
-    }
-    // this call's non-counter data starts right after its counters
-    d->zeroed = zero;
+    // (the step's QKV kernel clears the counters: no clearing here, so a
+    // captured graph of this call is complete)
     mb_decoder_step_args b = *a;
     b.workspace = d->ptr;
     b.workspace_bytes = NOALLOC_SCRATCH_BYTES;

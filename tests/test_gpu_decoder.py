@@ -165,6 +165,11 @@ def test_decoder_step_padded_stride_and_caller_workspace(mb, dev):
     # the caller's workspace is left ready: a second call gives the same bits
     for g1, g2 in zip(got_ws, _run(dev, ins, B, D, H, HKV, FF, L, stride=S, workspace=ws)):
         assert torch.equal(g1, g2)
+    # and it needs no initialisation: a workspace of 0xff bytes (every counter
+    # far from zero) gives the same bits too
+    junk = torch.full((nbytes,), 255, dtype=torch.uint8, device=dev)
+    for g1, g2 in zip(got_ws, _run(dev, ins, B, D, H, HKV, FF, L, stride=S, workspace=junk)):
+        assert torch.equal(g1, g2)
 
 
 def test_decoder_step_repeat_calls_bit_identical(mb, dev):

@@ -62,31 +62,39 @@ def test_noalloc_matches_allocating_entry_point(mb, dev):
             assert torch.equal(g, w), f"{cfg} {name}: no-alloc result differs"
 
 
-def test_noalloc_step_replays_from_a_captured_graph(mb, dev):
-    """The entry point's purpose: a caller that captures the step in a HIP
-    graph.  One eager call (which also clears the scratch counters), then a
-    capture, then three replays with eager work and synchronisation between
-    them; every replay must reproduce the eager outputs bit for bit."""
-    print("[no-alloc] graph capture and replays", flush=True)
+def test_noalloc_step_replays_from_captured_graphs(mb, dev):
+    """The entry point's purpose: callers that capture the step in HIP graphs
+    (one per shape, as serving loops do).  Two shapes are captured after one
+    eager call each; the graphs are then replayed three times each,
+    interleaved with eager calls of a smaller third shape on the same
+    scratch, with synchronisation between; every replay must reproduce the
+    eager outputs bit for bit."""
+    print("[no-alloc] graph capture and interleaved replays", flush=True)
     lib = native.load()
-    a, d, outs = _args(dev, (4, 512, 4, 2, 512, 70), 7)
-    _call("mb_launch_llama_decoder_step_bf16_noalloc", a)
-    want = [t.clone() for t in outs]
-    stream = torch.cuda.Stream()
-    graph = torch.cuda.CUDAGraph()
-    torch.cuda.synchronize()
-    with torch.cuda.graph(graph, stream=stream):
-        rc = lib.mb_launch_llama_decoder_step_bf16_noalloc(
-            ctypes.byref(a), ctypes.c_void_p(stream.cuda_stream))
-    assert rc == 0, native.last_error()
+    fn = lib.mb_launch_llama_decoder_step_bf16_noalloc
+    cases = []
+    for seed, cfg in ((7, (4, 512, 4, 2, 512, 70)), (8, (16, 2048, 16, 4, 1536, 300))):
+        a, d, outs = _args(dev, cfg, seed)
+        _call("mb_launch_llama_decoder_step_bf16_noalloc", a)
+        want = [t.clone() for t in outs]
+        stream = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            rc = fn(ctypes.byref(a), ctypes.c_void_p(stream.cuda_stream))
+        assert rc == 0, native.last_error()
+        cases.append((cfg, graph, outs, want, a, d))
+    a3, d3, outs3 = _args(dev, (2, 256, 2, 1, 256, 10), 9)
     for rep in range(3):
-        for t in outs:
-            t.fill_(float("nan"))
-        torch.cuda.synchronize()
-        graph.replay()
-        torch.cuda.synchronize()
-        for g, w, name in zip(outs, want, ("y", "k_new", "v_new")):
-            assert torch.equal(g, w), f"replay {rep} {name}: differs from the eager call"
+        for cfg, graph, outs, want, _, _ in reversed(cases):
+            _call("mb_launch_llama_decoder_step_bf16_noalloc", a3)   # other shapes in between
+            for t in outs:
+                t.fill_(float("nan"))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            for g, w, name in zip(outs, want, ("y", "k_new", "v_new")):
+                assert torch.equal(g, w), f"replay {rep} {cfg} {name}: differs from the eager call"
 
 
 def test_noalloc_rejects_oversized_shapes_and_a_workspace(mb, dev):
