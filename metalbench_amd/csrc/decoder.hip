@@ -248,7 +248,8 @@ struct GemmCfg {
     uint32_t ldw;
     uint32_t k;
     SplitGeom sp;
-    uint32_t paired;       // 1: tile t = gate cols [64t, 64t+64) + up cols ff + [64t, 64t+64)
+    uint32_t paired;       // 1: tile t of TBN columns = gate cols [h t, h t + h) + up cols
+                           //    ff + [h t, h t + h), h = TBN / 2
     uint32_t* counters;    // [tiles]
 };
 
@@ -704,7 +705,7 @@ void attention_kernel(StepParams p) {
     // The QKV GEMM leaves split-K partials, [tile][split][16][128] fp32 with
     // tile = one head of Q, K or V, and per-split row sums of x^2.  Every
     // workgroup of the pair sums row b of its G query heads, its key head and
-    // its value head over the splits (left to right, in batches of 8: loads
+    // its value head over the splits (left to right, in batches of PB: loads
     // past the last split return zeros), applies the RMSNorm row scale and
     // the RoPE rotation, and keeps q (pre-scaled by 1/sqrt(Dh), the MFMA B
     // operand, re-read per block), k_new and v_new as bf16 in LDS.  These
