@@ -36,6 +36,11 @@ $(OBJ_DIR)/%.hip.o: $(SRC_DIR)/%.hip $(HEADERS)
 	@mkdir -p $(OBJ_DIR)
 	$(HIPCC) $(HIPFLAGS) -c $< -o $@
 
+# decoder.hip: the skinny GEMM's 12 leading scalar and pointer arguments are
+# preloaded into SGPRs (its other kernels start with a struct argument, which
+# is not preloaded).
+$(OBJ_DIR)/decoder.hip.o: HIPFLAGS += -mllvm -amdgpu-kernarg-preload-count=12
+
 # Per-kernel register/LDS table of the kernels above, read from their own code
 # objects, compiled into runtime.cpp (mb_kernel_attrs_get).
 KERNEL_OBJS := $(filter-out $(OBJ_DIR)/runtime.cpp.o,$(HIP_OBJS))
