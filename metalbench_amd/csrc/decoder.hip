@@ -1200,6 +1200,10 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
             (uint64_t)B * k * 2 >= 0x80000000ull)
             return fail(MB_E_ARG, "decoder step: shapes too large for 32-bit weight offsets");
         plan_slow_class(pl, i, k, ldw[i], i == EPI_GU, i == EPI_GU ? 2 * FF : 0);
+        // (the skinny GEMM's preloaded arguments pack these in 16-bit fields)
+        if (pl->geo[i].kc_slow / KG > 0xffffu || pl->geo[i].kc / KG > 0xffffu ||
+            pl->geo[i].splits_slow > 0xffffu)
+            return fail(MB_E_ARG, "decoder step: K split geometry too large");
     }
     size_t max_part = 0;
     for (int i = 0; i < 4; ++i)
