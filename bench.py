@@ -19,8 +19,8 @@ R device copies of its working set (R x 570 MB for the decoder, R x 536 MB for
 the transpose), through the typed C entry point, so the 256 MB memory-side
 cache cannot serve one step from the previous one; the others reuse one set
 of buffers through mb_run.  Then K more
-steps run with a hipEvent pair per step (and a mark before each kernel of a
-multi-kernel step): `roofline.achieved` is the algorithmic bytes (HBM-bound
+steps run with a hipEvent pair per step (and, for the decode step, each
+kernel's own start and end events, which give `parts`): `roofline.achieved` is the algorithmic bytes (HBM-bound
 kernels) or flops (MFMA-bound kernels) of ONE launch of the dominant kernel
 divided by that kernel's mean event-timed duration over those K steps.
 
@@ -404,8 +404,9 @@ def _run_workload(name, steps, warmup, want_cpu, settle_ms):
     device_ms = ev0.elapsed_time(ev1) / steps
     native.load().mb_set_stream(None)
     # Per-kernel durations (roofline): `steps` more steps with a hipEvent pair
-    # per step and a mark before each kernel of the step; rotating workloads
-    # run them one by one over the copies, so each is timed cold as well.
+    # per step and per-kernel events (the decode step's kernels carry their
+    # own start and end events); rotating workloads run them one by one over
+    # the copies, so each is timed cold as well.
     if R > 1:
         k_t = _mean_timing([native.run(kid, bind_sets[i % R], 0, 1,
                                        native.RUN_PIPELINED | native.RUN_PARTS)

@@ -75,7 +75,10 @@ typedef struct mb_binding {
  * library stream; min / median (= sorted[n/2]) / mean over `iters`, the
  * statistics of reference metal/scripts/timing.mm:150-159 (TimingResult,
  * timing.h:24-33).  Multi-kernel entries also report per-kernel ("part")
- * times when MB_RUN_PARTS is set. */
+ * times when MB_RUN_PARTS is set: for the decode step each kernel's own
+ * start-to-end time (hipExtLaunchKernel events, nothing enqueued between the
+ * kernels), for the others the time from one kernel's start to the next's
+ * (so it includes the dispatch gap). */
 typedef struct mb_timing {
     double  min_ms;
     double  median_ms;

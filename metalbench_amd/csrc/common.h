@@ -50,16 +50,33 @@ void* library_flush_buffer(size_t* bytes);
 int launch_cache_eviction(hipStream_t s);
 
 // ---- per-kernel timing marks ---------------------------------------------------
-// A multi-kernel entry calls mark(i, name) right before enqueuing kernel i.
-// When timing parts, mb_run records an event there.
+// A multi-kernel entry names each part right before enqueuing it, in one of
+// two ways.  mark(name): when timing parts, mb_run records an event there,
+// and the part runs to the next part's start (so it includes the dispatch
+// gap before the next kernel).  kernel(name, &start, &stop): the entry
+// launches the part's one kernel with hipExtLaunchKernel and these events,
+// which take that kernel's own start and end times (no extra packet between
+// kernels), or with a plain launch when both come back null.
 struct PartMarks {
-    hipEvent_t* events = nullptr;   // n_max events, or nullptr
+    hipEvent_t* events = nullptr;   // n_max start events, or nullptr
+    hipEvent_t* stops = nullptr;    // n_max stop events (kernel parts)
     int n_max = 0;
     int n = 0;
     const char* names[MB_MAX_PARTS] = {};
+    bool own_kernel[MB_MAX_PARTS] = {};   // part timed by its kernel's own events
     void mark(hipStream_t s, const char* name) {
         if (n < MB_MAX_PARTS) names[n] = name;
         if (events && n < n_max) (void)hipEventRecord(events[n], s);
+        ++n;
+    }
+    void kernel(const char* name, hipEvent_t* start, hipEvent_t* stop) {
+        *start = *stop = nullptr;
+        if (n < MB_MAX_PARTS) names[n] = name;
+        if (events && stops && n < n_max) {
+            *start = events[n];
+            *stop = stops[n];
+            own_kernel[n] = true;
+        }
         ++n;
     }
 };

@@ -47,6 +47,8 @@
 // reads them.  Details at skinny_gemm_kernel.
 #include "common.h"
 
+#include <hip/hip_ext.h>
+
 #include <math.h>
 
 #include <algorithm>
@@ -1237,8 +1239,17 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
 }
 
 
+// A launch timed by its own start/stop events when they are given (per-part
+// timing, PartMarks::kernel), a plain launch otherwise.
+#define LAUNCH_TIMED(kern, grid, block, s, e0, e1, ...)                                    \
+    do {                                                                                   \
+        if (e0) hipExtLaunchKernelGGL(kern, grid, block, 0, s, e0, e1, 0, __VA_ARGS__);  \
+        else hipLaunchKernelGGL(kern, grid, block, 0, s, __VA_ARGS__);                     \
+    } while (0)
+
 template <int EPI, int WW>
-void launch_skinny_ww(const GemmCfg& g, uint32_t ring, const StepParams& p, hipStream_t s) {
+void launch_skinny_ww(const GemmCfg& g, uint32_t ring, const StepParams& p, hipStream_t s,
+                      hipEvent_t e0, hipEvent_t e1) {
     const dim3 grid(grid_blocks(g.sp)), block(256);
     SkinnyPre q;
     q.w = g.w; q.a = g.a;
@@ -1253,18 +1264,19 @@ void launch_skinny_ww(const GemmCfg& g, uint32_t ring, const StepParams& p, hipS
     q.cls = g.sp.slow_mask | g.sp.slow_val << 16;
     q.ff = p.ff;
     switch (ring) {
-        case 1: hipLaunchKernelGGL((skinny_gemm_kernel<EPI, WW, 1>), grid, block, 0, s, SKINNY_PRE_ARGS(q), g, p); break;
-        case 2: hipLaunchKernelGGL((skinny_gemm_kernel<EPI, WW, 2>), grid, block, 0, s, SKINNY_PRE_ARGS(q), g, p); break;
-        default: hipLaunchKernelGGL((skinny_gemm_kernel<EPI, WW, RING>), grid, block, 0, s, SKINNY_PRE_ARGS(q), g, p); break;
+        case 1: LAUNCH_TIMED((skinny_gemm_kernel<EPI, WW, 1>), grid, block, s, e0, e1, SKINNY_PRE_ARGS(q), g, p); break;
+        case 2: LAUNCH_TIMED((skinny_gemm_kernel<EPI, WW, 2>), grid, block, s, e0, e1, SKINNY_PRE_ARGS(q), g, p); break;
+        default: LAUNCH_TIMED((skinny_gemm_kernel<EPI, WW, RING>), grid, block, s, e0, e1, SKINNY_PRE_ARGS(q), g, p); break;
     }
 }
 
 template <int EPI>
-void launch_skinny(const GemmCfg& g, const Plan& pl, const StepParams& p, hipStream_t s) {
+void launch_skinny(const GemmCfg& g, const Plan& pl, const StepParams& p, hipStream_t s,
+                   hipEvent_t e0, hipEvent_t e1) {
     if constexpr (EPI == EPI_GU) {
-        if (pl.ww[EPI] == 4) return launch_skinny_ww<EPI, 4>(g, pl.ring[EPI], p, s);
+        if (pl.ww[EPI] == 4) return launch_skinny_ww<EPI, 4>(g, pl.ring[EPI], p, s, e0, e1);
     }
-    launch_skinny_ww<EPI, 1>(g, pl.ring[EPI], p, s);
+    launch_skinny_ww<EPI, 1>(g, pl.ring[EPI], p, s, e0, e1);
 }
 
 int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) {
@@ -1351,26 +1363,28 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
     p.next[EPI_WO] = next_units(EPI_WO, a->w_o, D, QD, 0);
     p.next[EPI_GU] = next_units(EPI_GU, a->w_gu, 2 * FF, D, 2 * FF);
     p.next[EPI_DOWN] = next_units(EPI_DOWN, a->w_down, D, FF, 0);
-    auto mark = [&](const char* name) { if (pm) pm->mark(s, name); };
-    mark("qkv");
-    launch_skinny<EPI_QKV>(g_qkv, pl, p, s);
+    // each part is one kernel; when parts are timed, by its own events
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    auto part = [&](const char* name) { if (pm) pm->kernel(name, &e0, &e1); };
+    part("qkv");
+    launch_skinny<EPI_QKV>(g_qkv, pl, p, s, e0, e1);
     MB_LAUNCH_CHECK("decoder qkv");
-    mark("attention");
+    part("attention");
     {
         const dim3 grid(a->batch * a->n_kv_heads * pl.nsplit), block(256);
-        if (pl.g <= 4) hipLaunchKernelGGL(attention_kernel<4>, grid, block, 0, s, p);
-        else if (pl.g <= 8) hipLaunchKernelGGL(attention_kernel<8>, grid, block, 0, s, p);
-        else hipLaunchKernelGGL(attention_kernel<16>, grid, block, 0, s, p);
+        if (pl.g <= 4) LAUNCH_TIMED(attention_kernel<4>, grid, block, s, e0, e1, p);
+        else if (pl.g <= 8) LAUNCH_TIMED(attention_kernel<8>, grid, block, s, e0, e1, p);
+        else LAUNCH_TIMED(attention_kernel<16>, grid, block, s, e0, e1, p);
     }
     MB_LAUNCH_CHECK("decoder attention");
-    mark("wo_residual");
-    launch_skinny<EPI_WO>(g_wo, pl, p, s);
+    part("wo_residual");
+    launch_skinny<EPI_WO>(g_wo, pl, p, s, e0, e1);
     MB_LAUNCH_CHECK("decoder wo_residual");
-    mark("gate_up_swiglu");
-    launch_skinny<EPI_GU>(g_gu, pl, p, s);
+    part("gate_up_swiglu");
+    launch_skinny<EPI_GU>(g_gu, pl, p, s, e0, e1);
     MB_LAUNCH_CHECK("decoder gate_up_swiglu");
-    mark("down_residual");
-    launch_skinny<EPI_DOWN>(g_dn, pl, p, s);
+    part("down_residual");
+    launch_skinny<EPI_DOWN>(g_dn, pl, p, s, e0, e1);
     MB_LAUNCH_CHECK("decoder down_residual");
     return MB_OK;
 }

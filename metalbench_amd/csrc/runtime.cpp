@@ -416,8 +416,9 @@ int mb_run(int id, const mb_binding* bindings, int n_bindings, int warmup, int i
     const bool pipelined = flags & MB_RUN_PIPELINED;
     const bool parts = (flags & MB_RUN_PARTS) && k.n_parts > 1;
     const int np = parts ? std::min(k.n_parts, MB_MAX_PARTS) : 0;
-    // Events: per iteration a start/stop pair, plus np-1 interior marks.
-    const int per_iter = 2 + (np > 1 ? np - 1 : 0);
+    // Events per iteration: the region's start, np part starts, np part stops
+    // (used by parts that time their own kernel) and the region's stop.
+    const int per_iter = 2 + (np > 1 ? 2 * np : 0);
     const int n_ev = pipelined ? per_iter * iters : per_iter;
     std::vector<hipEvent_t> ev(n_ev);
     for (auto& e : ev) MB_HIP_TRY(hipEventCreate(&e));
@@ -426,6 +427,7 @@ int mb_run(int id, const mb_binding* bindings, int n_bindings, int warmup, int i
     std::vector<double> times(iters);
     std::vector<std::vector<double>> part_times(np, std::vector<double>(iters));
     const char* part_names[MB_MAX_PARTS] = {};
+    bool part_own[MB_MAX_PARTS] = {};
 
     auto collect = [&](hipEvent_t* e, int it) -> int {
         float ms = 0.f;
@@ -433,9 +435,11 @@ int mb_run(int id, const mb_binding* bindings, int n_bindings, int warmup, int i
         if (r != hipSuccess) return fail(MB_E_HIP, "hipEventElapsedTime: %s", hipGetErrorString(r));
         times[it] = ms;
         for (int p = 0; p < np; ++p) {
-            // part p runs from mark p (event 0 for p == 0) to mark p+1 (stop for the last).
-            hipEvent_t a = p == 0 ? e[0] : e[p];
-            hipEvent_t b = p == np - 1 ? e[per_iter - 1] : e[p + 1];
+            // a part timed by its kernel's own events runs from that kernel's
+            // start to its end; a marked part from its start to the next
+            // part's start (the region's stop for the last)
+            hipEvent_t a = e[1 + p];
+            hipEvent_t b = part_own[p] ? e[1 + np + p] : p == np - 1 ? e[per_iter - 1] : e[2 + p];
             r = hipEventElapsedTime(&ms, a, b);
             if (r != hipSuccess) return fail(MB_E_HIP, "hipEventElapsedTime: %s", hipGetErrorString(r));
             part_times[p][it] = ms;
@@ -453,10 +457,15 @@ int mb_run(int id, const mb_binding* bindings, int n_bindings, int warmup, int i
         hipError_t r = hipEventRecord(e[0], s);
         if (r != hipSuccess) { destroy(); return fail(MB_E_HIP, "hipEventRecord: %s", hipGetErrorString(r)); }
         PartMarks pm;
-        if (np > 1) { pm.events = e; pm.n_max = np; }   // mark 0 re-records e[0]: harmless
+        if (np > 1) { pm.events = e + 1; pm.stops = e + 1 + np; pm.n_max = np; }
         int rc = k.launch(bs, s, np > 1 ? &pm : nullptr);
         if (rc) { destroy(); return rc; }
-        if (np > 1) for (int p = 0; p < np && p < pm.n; ++p) part_names[p] = pm.names[p];
+        if (np > 1 && pm.n < np) {   // a part that was never started has no events
+            destroy();
+            return fail(MB_E_HIP, "kernel %s started %d of its %d timed parts", k.name, pm.n, np);
+        }
+        if (np > 1)
+            for (int p = 0; p < np; ++p) { part_names[p] = pm.names[p]; part_own[p] = pm.own_kernel[p]; }
         r = hipEventRecord(e[per_iter - 1], s);
         if (r != hipSuccess) { destroy(); return fail(MB_E_HIP, "hipEventRecord: %s", hipGetErrorString(r)); }
         if (!pipelined) {
