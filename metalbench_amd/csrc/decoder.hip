@@ -308,7 +308,7 @@ __device__ __forceinline__ uint32_t tile_col(const GemmCfg& g, uint32_t ff, uint
 struct SkinnyPre {
     const uint16_t* w;
     const uint16_t* a;
-    uint32_t a_lo_off;   // bytes from a to a_lo (hi + lo activations)
+    uint32_t a_lo_off;   // bytes from a to a_lo (hi + lo activations; a_lo follows a in the workspace)
     uint32_t ldw, lda, k;
     uint32_t batch_paired;   // batch | paired << 16
     uint32_t tiles, splits;  // splits | splits_slow << 16
