@@ -249,3 +249,22 @@ def test_decoder_step_rope_at_large_position(mb, dev):
     bad = np.abs(kn - wk) > 2.0 ** -8 * np.abs(wk) + 1e-4 * pair
     assert not bad.any(), f"k_new: {int(bad.sum())} of {kn.size} beyond bf16 rounding, " \
                           f"max |diff| {np.abs(kn - wk).max():.3e}"
+
+
+def test_decoder_parts_time_each_kernel_alone(mb):
+    """mb_run with MB_RUN_PARTS: the decode step reports its five kernels by
+    name, each timed by its own start and end events (hipExtLaunchKernel), so
+    every part is positive and the parts sum to less than the whole dispatch,
+    which also holds the dispatch gaps between them.  The outputs of a timed
+    run are the step's (checked against the oracle at the registry shape by
+    test_decoder_step_registry_config)."""
+    from metalbench_amd import harness
+    from metalbench_amd import helpers as H
+    b = H.load_baseline("llama_decoder_step_tp8")
+    k_t, outs = harness._run_native(b, b.make_inputs(0), 1, 5,
+                                    native.RUN_PIPELINED | native.RUN_PARTS)
+    names = [p["name"] for p in k_t["parts"]]
+    assert names == ["qkv", "attention", "wo_residual", "gate_up_swiglu", "down_residual"]
+    assert all(p["mean_ms"] > 0 for p in k_t["parts"]), k_t["parts"]
+    assert sum(p["mean_ms"] for p in k_t["parts"]) < k_t["mean_ms"], k_t
+    assert all(torch.isfinite(o.float()).all() for o in outs)
