@@ -60,11 +60,15 @@ def _step_shape(meta: dict) -> dict:
 
 
 def _decoder_part_bytes(meta: dict | None = None) -> dict:
-    """Algorithmic HBM bytes of one launch of each decoder kernel: every weight
-    and cache byte once, activations in and out once (bf16 = 2 bytes).  The
-    attention width QD = H * Dh is D for a whole layer.  The QKV GEMM's
-    outputs reach the attention kernel as split-K partials (workspace traffic,
-    not counted)."""
+    """Bytes one launch of each decoder kernel must move, for the per-kernel
+    `hbm_frac` of `parts`: every weight and cache byte once, plus the kernel's
+    own activation inputs and outputs once at the width they are stored in
+    (bf16 = 2 bytes; the x1 residual is fp32 and written by W_o, read by
+    down).  The QKV GEMM's result reaches attention as split-K partials, which
+    neither side counts.  The step's headline roofline does not use these: it
+    is priced on the registry's algorithmic bytes (weights, caches, x, y, the
+    new k and v), which leave every intermediate out.  The attention width
+    QD = H * Dh is D for a whole layer."""
     if meta is None:
         from metalbench_amd import helpers as H
         meta = H.load_baseline("llama_decoder_step").meta
@@ -86,10 +90,11 @@ def _decoder_part_bytes(meta: dict | None = None) -> dict:
 def _work(name: str, meta: dict):
     if name in DECODE_STEPS:
         # The roofline is priced on the whole step (its five kernels and the
-        # dispatch gaps between them) over the back-to-back timed region; the
-        # per-kernel figures stay in `parts`.
-        parts = _decoder_part_bytes(meta)
-        return dict(part=None, bound="hbm", per_launch=sum(parts.values()), parts=parts,
+        # dispatch gaps between them) over the back-to-back timed region, with
+        # the registry's algorithmic bytes; the per-kernel figures stay in
+        # `parts`.
+        return dict(part=None, bound="hbm", per_launch=int(meta["bytes"]),
+                    parts=_decoder_part_bytes(meta),
                     label="decode step: qkv, attention, wo_residual, gate_up_swiglu, "
                           "down_residual")
     if _bound(meta) == "hbm":

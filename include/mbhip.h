@@ -229,12 +229,16 @@ int mb_launch_conv2d_nhwc_f32(const float* x, const float* w, float* y,
  *   - weights are x @ W layouts: w_qkv [D][QD + 2*Hkv*Dh] with columns
  *     [Q | K | V], w_gu [D][2*FF] with columns [gate | up] (reference
  *     llama_decoder_layer.py:30-32, 43-44), QD = H * Dh.
- * For a whole layer QD = D.  QD < D is one tensor-parallel shard of a layer:
- * its H of the query heads and Hkv of the kv heads (w_qkv's columns), its
- * QD rows of W_o and its FF columns of gate and up (FF rows of W_down); the
- * step then computes that shard's work with the two all-reduces (after W_o
- * and after W_down) left to the caller, i.e. y = x1 + act @ W_down with
- * x1 = x + attn @ W_o on the shard's partial products.
+ * For a whole layer QD = D.  QD < D runs the work of one GPU's share of a
+ * tensor-parallel layer at its real shapes (its H query heads and Hkv kv
+ * heads in w_qkv's columns, its QD rows of W_o, its FF columns of gate and up
+ * and FF rows of W_down): a per-shard cost proxy for benchmarking, NOT a
+ * building block of a tensor-parallel step.  The call still adds the full
+ * residual x and normalises its own partial x1 = x + attn @ W_o, so the sum
+ * of the shards' y is not the layer's output.  A real shard needs the step
+ * split at W_o, with the all-reduce of attn @ W_o between the two halves, the
+ * FFN's RMSNorm on the all-reduced x1, and each residual added on one rank
+ * only; this library does not provide that split.
  * All tensors are row-major bf16 bit patterns.  The caches are read only; the
  * new token's RoPE'd key and its value are written to k_new / v_new so the
  * caller can append them. */

@@ -38,10 +38,10 @@ hipStream_t stream_or_default(void* s);   // NULL -> current library stream
 uint32_t device_cu_count();               // compute units of the initialised device
 
 // Library-owned device workspace, grown on demand, freed by mb_shutdown().
-// The first `zero_prefix` bytes are guaranteed zero the first time they are
-// handed out (cleared on stream `s`); the caller must leave them zero again.
-// Returns nullptr (and sets the error) on failure.
-void* library_workspace(size_t bytes, size_t zero_prefix, hipStream_t s);
+// Its contents are undefined when handed out: a kernel that needs zeroed
+// counters clears them itself.  Returns nullptr (and sets the error) on
+// failure.
+void* library_workspace(size_t bytes);
 
 // Library-owned buffer twice the size of the memory-side cache, allocated on
 // first use and freed by mb_shutdown(); writing it evicts every cache level.

@@ -1298,7 +1298,7 @@ int launch_decoder(const mb_decoder_step_args* a, hipStream_t s, PartMarks* pm) 
             return fail(MB_E_ARG, "decoder step: workspace %llu bytes, need %zu",
                         (unsigned long long)a->workspace_bytes, pl.total);
     } else {
-        ws = static_cast<uint8_t*>(library_workspace(pl.total, 0, s));
+        ws = static_cast<uint8_t*>(library_workspace(pl.total));
         if (!ws) return MB_E_HIP;
     }
 

@@ -40,7 +40,6 @@ struct State {
     hipStream_t user_stream = nullptr;
     void* ws = nullptr;
     size_t ws_bytes = 0;
-    size_t ws_zeroed = 0;   // bytes at the front of ws known to be zero
     void* flush = nullptr;  // cache-eviction buffer (MB_RUN_COLD)
     uint32_t cu_count = 0;
 };
@@ -55,7 +54,7 @@ hipStream_t stream_or_default(void* s) {
     return g.user_stream ? g.user_stream : g.lib_stream;
 }
 
-void* library_workspace(size_t bytes, size_t zero_prefix, hipStream_t s) {
+void* library_workspace(size_t bytes) {
     if (bytes > g.ws_bytes) {
         if (g.ws) {
             // The old workspace may still be read by enqueued work.
@@ -63,7 +62,6 @@ void* library_workspace(size_t bytes, size_t zero_prefix, hipStream_t s) {
             (void)hipFree(g.ws);
             g.ws = nullptr;
             g.ws_bytes = 0;
-            g.ws_zeroed = 0;
         }
         hipError_t e = hipMalloc(&g.ws, bytes);
         if (e != hipSuccess) {
@@ -73,20 +71,6 @@ void* library_workspace(size_t bytes, size_t zero_prefix, hipStream_t s) {
         }
         g.ws_bytes = bytes;
     }
-    if (zero_prefix > g.ws_zeroed) {
-        // Counters live at the front of the workspace and are left at zero by
-        // the kernels that use them; bytes past the last caller's counters may
-        // hold its scratch data, so they are cleared (in stream order) before
-        // they serve as counters.
-        hipError_t e = hipMemsetAsync(static_cast<uint8_t*>(g.ws) + g.ws_zeroed, 0,
-                                      zero_prefix - g.ws_zeroed, s);
-        if (e != hipSuccess) {
-            fail(MB_E_HIP, "workspace clear failed: %s", hipGetErrorString(e));
-            return nullptr;
-        }
-    }
-    // This caller writes non-counter data right after its own counters.
-    g.ws_zeroed = zero_prefix;
     return g.ws;
 }
 

@@ -443,7 +443,7 @@ int run_llama_attention(const Bindings& bs, hipStream_t s, PartMarks*) {
         (rc = bs.buffer(3, MB_DTYPE_F32, (uint64_t)S * D * 4, true, &y, "y")))
         return rc;
     const size_t qkv_bytes = ((size_t)S * nqkv * 4 + 255) & ~(size_t)255;
-    uint8_t* ws = static_cast<uint8_t*>(library_workspace(qkv_bytes + (size_t)S * D * 4, 0, s));
+    uint8_t* ws = static_cast<uint8_t*>(library_workspace(qkv_bytes + (size_t)S * D * 4));
     if (!ws) return MB_E_HIP;
     float* qkv = reinterpret_cast<float*>(ws);
     float* attn = reinterpret_cast<float*>(ws + qkv_bytes);
@@ -494,7 +494,7 @@ int run_llama_decoder_layer(const Bindings& bs, hipStream_t s, PartMarks* pm) {
     const size_t o_qkv = 0, o_attn = al((size_t)S * nqkv * 8),
                  o_x1 = o_attn + al((size_t)S * D * 4), o_act = o_x1 + al((size_t)S * D * 4),
                  total = o_act + al((size_t)S * FF * 4);
-    uint8_t* ws = static_cast<uint8_t*>(library_workspace(total, 0, s));
+    uint8_t* ws = static_cast<uint8_t*>(library_workspace(total));
     if (!ws) return MB_E_HIP;
     double* qkv = reinterpret_cast<double*>(ws + o_qkv);
     float* attn = reinterpret_cast<float*>(ws + o_attn);

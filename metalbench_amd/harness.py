@@ -3,6 +3,7 @@
     python mlx/scripts/harness.py <name> [--target speed|compute|memory|stable|balanced]
                                          [--iters 200] [--warmup 10] [--seed 0]
                                          [--save] [--no-session] [--dry-run] [--cold-start]
+                                         [--profile] [--xcode | --gputracer] [--capture-host DIR]
                                          [--mlx-only | --metal-only] [--cpu-iters N]
 
 Same flow, report text, exit codes and persistence as reference
@@ -14,7 +15,10 @@ mlx/scripts/harness.py:52-508, with the gfx950 backend in place of Metal:
     the same spec's output, in float64, with the reference's rule
     |a - b| <= atol + rtol*|b| (reference :26-33);
   * the `roofline` line prices the kernel against MI355X peaks for the dtype
-    it computes in.
+    it computes in;
+  * `--profile` and `--capture-host` / `--xcode` run one more dispatch in a
+    child process under rocprofv3 (counters, or a kernel trace) instead of
+    sampling MTLCounterSet or recording a .gputrace in the host.
 `--metal-only` / `--mlx-only` keep their reference meaning: the GPU kernel only
 (no spec timing, no correctness gate) / the CPU spec only.
 """
@@ -101,7 +105,7 @@ def _cpu_iters(b, iters, override):
 
 
 def evaluate(name, *, seed, warmup, iters, dry_run=False, profile=False, solo=None,
-             cpu_iters=None, cold_start=False):
+             cpu_iters=None, cold_start=False, capture_host=None):
     b = H.load_baseline(name)
     inputs = b.make_inputs(seed)
     # --mlx-only and --dry-run make no GPU call
@@ -121,7 +125,8 @@ def evaluate(name, *, seed, warmup, iters, dry_run=False, profile=False, solo=No
                 "outputs": []}
 
     manifest = H.build_manifest(b, inputs, warmup=warmup, iters=iters,
-                                chip_type=chip["type"], profile=profile)
+                                chip_type=chip["type"], profile=profile,
+                                capture_host=capture_host)
     if dry_run:
         return {"task": name, "dry_run": True, "manifest": manifest}
 
@@ -134,6 +139,9 @@ def evaluate(name, *, seed, warmup, iters, dry_run=False, profile=False, solo=No
                                    native.RUN_COLD if cold_start else native.RUN_SYNC_EACH)
     if cold_start:
         k_t["cold_start"] = True
+    # the reference host records its trace after the timed dispatches
+    # (main.mm:173-177), in every mode that runs the kernel
+    capture = capture_dispatch(name, seed, capture_host) if capture_host else None
 
     def _kernel_metrics(m):
         median_s = k_t["median_ms"] / 1000.0
@@ -150,9 +158,12 @@ def evaluate(name, *, seed, warmup, iters, dry_run=False, profile=False, solo=No
         return m
 
     if solo == "metal":
-        return {"task": name, "chip": chip, "solo": "metal", "correct": True,
-                "metrics": _kernel_metrics({}), "kernel_timing": k_t, "outputs": [],
-                "compute_dtype": b.compute_dtype}
+        out = {"task": name, "chip": chip, "solo": "metal", "correct": True,
+               "metrics": _kernel_metrics({}), "kernel_timing": k_t, "outputs": [],
+               "compute_dtype": b.compute_dtype}
+        if capture is not None:
+            out["capture"] = capture
+        return out
 
     ref_out = b.reference(*inputs)
     ref_outs = list(ref_out) if isinstance(ref_out, (list, tuple)) else [ref_out]
@@ -189,9 +200,13 @@ def evaluate(name, *, seed, warmup, iters, dry_run=False, profile=False, solo=No
         "outputs": per_output,
         "compute_dtype": b.compute_dtype,
     }
-    # The reference host always emits a profiling block (main.mm:183-195);
-    # with --profile it holds counters, here from rocprofv3 passes.
+    # The reference host always emits the available counter sets and a
+    # profiling block (main.mm:181-195); with --profile the block holds
+    # counters, here from rocprofv3 passes.
+    result["available_counter_sets"] = available_counter_sets()
     result["profiling"] = profile_counters(name, seed) if profile else {"counters_available": False}
+    if capture is not None:
+        result["capture"] = capture
     return result
 
 
@@ -208,6 +223,16 @@ PROFILE_PASSES = (
      "SQ_WAIT_INST_LDS", "SQ_WAIT_INST_ANY", "FETCH_SIZE"),
     ("WRITE_SIZE",),
 )
+
+
+def available_counter_sets() -> list:
+    """What `--profile` can sample on this host: the counters of its
+    rocprofv3 passes, or nothing without rocprofv3 (the reference lists the
+    device's MTLCounterSets, main.mm:40-51)."""
+    import shutil
+    if not shutil.which("rocprofv3"):
+        return []
+    return [c for p in PROFILE_PASSES for c in p]
 
 
 def parse_counter_csv(path) -> dict:
@@ -251,6 +276,59 @@ def profile_counters(name, seed, timeout_s=120) -> dict:
     names = [c for p in PROFILE_PASSES for c in p]
     return {"counters_available": True, "counter_set": "rocprofv3 --pmc (" + ", ".join(names) + ")",
             "samples": [{"name": c, "value": int(values.get(c, 0))} for c in names]}
+
+
+# ---- --capture-host / --xcode: a kernel trace of one dispatch --------------------------
+# The reference records a .gputrace of one extra dispatch (timing.mm:199-229,
+# reached through the manifest's capture_path, main.mm:173-177).  Here the
+# registry kernel runs once more in a child process under
+# `rocprofv3 --kernel-trace --stats`, which writes its CSV files into the
+# capture directory; the report names the kernels of that dispatch.
+def parse_kernel_trace_csv(path) -> list:
+    """This library's kernels in a rocprofv3 kernel_trace.csv, in dispatch
+    order: [{"name", "duration_ns"}]."""
+    import csv
+    rows = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            if "mb::" not in r.get("Kernel_Name", ""):
+                continue
+            rows.append((int(r.get("Dispatch_Id") or 0), r["Kernel_Name"],
+                         int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+    rows.sort()
+    return [{"name": n, "duration_ns": d} for _, n, d in rows]
+
+
+def capture_dispatch(name, seed, trace_path, timeout_s=180) -> dict:
+    import shutil
+    import subprocess
+    out = Path(trace_path).resolve()
+    exe = shutil.which("rocprofv3")
+    if not exe:
+        print("[host] capture unavailable: rocprofv3 not found", file=sys.stderr)
+        return {"written": False, "path": str(out), "reason": "rocprofv3 not found"}
+    out.mkdir(parents=True, exist_ok=True)
+    env = dict(os.environ, TMPDIR="/tmp")
+    cmd = [exe, "--kernel-trace", "--stats", "-f", "csv", "-d", str(out), "-o", name, "--",
+           sys.executable, str(H.REPO_ROOT / "mlx" / "scripts" / "harness.py"), name,
+           "--metal-only", "--warmup", "0", "--iters", "1", "--seed", str(seed),
+           "--no-session"]
+    try:
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout_s,
+                           cwd="/tmp", env=env)
+    except subprocess.TimeoutExpired:
+        print(f"[host] capture unavailable: rocprofv3 timed out after {timeout_s} s",
+              file=sys.stderr)
+        return {"written": False, "path": str(out), "reason": "rocprofv3 timed out"}
+    found = sorted(out.rglob(f"{name}_kernel_trace.csv"))
+    if r.returncode != 0 or not found:
+        why = f"rocprofv3 exit {r.returncode}: {r.stderr.strip()[-200:]}"
+        print(f"[host] capture unavailable: {why}", file=sys.stderr)
+        return {"written": False, "path": str(out), "reason": why}
+    kernels = parse_kernel_trace_csv(found[-1])
+    print(f"[host] trace written: {out}", file=sys.stderr)
+    return {"written": True, "path": str(out), "files": [str(p) for p in sorted(out.rglob("*.csv"))],
+            "kernels": kernels}
 
 
 # Each target picks ONE primary metric to optimize (reference harness.py:176-186).
@@ -341,6 +419,18 @@ def _roofline_line(result, m, k_t):
     return roofline.format_line(rl)
 
 
+def _print_capture(cap):
+    if not cap:
+        return
+    if not cap.get("written"):
+        print(f"  trace       : unavailable ({cap.get('reason')})")
+        return
+    print(f"  trace       : {cap['path']}  (rocprofv3 kernel trace of one dispatch)")
+    for k in cap.get("kernels", []):
+        short = k["name"].replace("(anonymous namespace)::", "").split("(")[0]
+        print(f"    {short:40s} {k['duration_ns'] / 1000.0:10.1f} µs")
+
+
 def _print_report(result, target, score):
     """Human-readable report, same labels as reference harness.py:257-333."""
     chip = result["chip"]
@@ -367,6 +457,7 @@ def _print_report(result, target, score):
             print(f"  stability   : {m['stability']:.2f}")
         if solo == "metal":
             print(_roofline_line(result, m, k_t))
+            _print_capture(result.get("capture"))
         print(line)
         return
 
@@ -384,6 +475,8 @@ def _print_report(result, target, score):
                      f"  waves/simd={regs['waves_per_simd']}")
         print(f"  occupancy   : tg_mem={_bytes_human(result['tg_static_mem_bytes'])}  "
               f"max_thr/tg={result['pso_max_threads_per_tg']}{extra}")
+    if result.get("available_counter_sets"):
+        print(f"  counters    : {', '.join(result['available_counter_sets'])}")
     print()
     status = "✓ correct " if result["correct"] else "✗ INCORRECT"
     max_err = max((o["max_err"] for o in outs), default=0.0)
@@ -414,6 +507,7 @@ def _print_report(result, target, score):
             print(f"    {smp['name']:40s} {smp['value']}")
     elif prof.get("reason"):
         print(f"  profiling   : unavailable ({prof['reason']})")
+    _print_capture(result.get("capture"))
     print()
     print(f"  {'target':>10s}   {'score':>10s}")
     print(f"  {'-'*10}   {'-'*10}")
@@ -444,6 +538,11 @@ def main(argv=None):
                     help="no warmup; evict every cache level before each timed dispatch")
     ap.add_argument("--profile", action="store_true",
                     help="hardware counters of one extra dispatch, from rocprofv3 --pmc passes")
+    ap.add_argument("--capture-host", default=None, metavar="DIR",
+                    help="rocprofv3 kernel trace of one extra dispatch, written into DIR")
+    ap.add_argument("--xcode", "--gputracer", dest="xcode", action="store_true",
+                    help="kernel trace of one extra dispatch into results/<chip>/<name>.trace "
+                         "(--gputracer is an alias)")
     ap.add_argument("--save", action="store_true",
                     help="save full result JSON to results/<chip>/<name>.json")
     ap.add_argument("--no-session", action="store_true", help="don't update session.json")
@@ -482,9 +581,19 @@ def main(argv=None):
     except Exception:
         pass
 
+    # --xcode: the trace goes to results/<chip type>/<name>.trace unless
+    # --capture-host names a place (reference harness.py:455-464); there is no
+    # viewer to open, so the report prints its kernels instead
+    if args.xcode and args.capture_host is None:
+        args.capture_host = str(H.RESULTS_ROOT / chip["type"] / f"{args.name}.trace")
+        print(f"[xcode] will record a kernel trace → {args.capture_host}", file=sys.stderr)
+    if args.capture_host and solo_mode == "mlx":
+        print("[xcode] no trace: --mlx-only makes no GPU call", file=sys.stderr)
+
     result = evaluate(args.name, seed=args.seed, warmup=args.warmup, iters=args.iters,
                       dry_run=args.dry_run, profile=args.profile, solo=solo_mode,
-                      cpu_iters=args.cpu_iters, cold_start=args.cold_start)
+                      cpu_iters=args.cpu_iters, cold_start=args.cold_start,
+                      capture_host=args.capture_host)
 
     if args.dry_run:
         print(json.dumps(result["manifest"], indent=2))

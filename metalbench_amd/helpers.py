@@ -259,9 +259,12 @@ def load_baseline(name) -> Baseline:
     return Baseline(name, set_name, mod, meta, spec, scalars)
 
 
-def build_manifest(b: Baseline, inputs, *, warmup, iters, chip_type=None, profile=False):
+def build_manifest(b: Baseline, inputs, *, warmup, iters, chip_type=None, profile=False,
+                   capture_host=None):
     """The dispatch description (reference mlx_helpers.py:290-335) without file
-    paths: inputs and outputs are handed over as device buffers in-process."""
+    paths: inputs and outputs are handed over as device buffers in-process.
+    `capture_path` is present when a kernel trace of one dispatch is asked for
+    (reference :333-334)."""
     buffers = []
     for binding, t, dt in zip(b.input_bindings, inputs, b.input_dtypes):
         buffers.append({"binding": int(binding), "role": "input", "dtype": dt,
@@ -279,7 +282,7 @@ def build_manifest(b: Baseline, inputs, *, warmup, iters, chip_type=None, profil
         if override:
             threadgroup = list(override.get("threadgroup", threadgroup))
             grid = list(override.get("grid", grid))
-    return {
+    manifest = {
         "function": b.metal_function,
         "library": "metalbench_amd/lib/libmbhip.so",
         "buffers": buffers,
@@ -289,6 +292,9 @@ def build_manifest(b: Baseline, inputs, *, warmup, iters, chip_type=None, profil
         "iters": int(iters),
         "profile": bool(profile),
     }
+    if capture_host:
+        manifest["capture_path"] = str(capture_host)
+    return manifest
 
 
 def find_kernel_source(name: str) -> Path | None:

@@ -17,8 +17,10 @@ import torch.nn.functional as F
 class Model(torch.nn.Module):
     """One decode step of a LLaMA decoder layer.
 
-    Inputs (QD = H * D_head; QD = D for a whole layer, QD < D for one
-    tensor-parallel shard computed alone, without the all-reduces):
+    Inputs (QD = H * D_head; QD = D for a whole layer, QD < D for the work
+    of one tensor-parallel shard at its real shapes -- a cost proxy: the full
+    residual is added and the shard's own partial x1 normalised, so shards'
+    outputs do not sum to the layer's):
         x        (B, D)
         W_qkv    (D, QD + 2*H_kv*D_head)  columns [Q | K | V]
         W_o      (QD, D)

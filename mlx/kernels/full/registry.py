@@ -61,8 +61,10 @@ _decode_step("llama_decoder_step", 16, 4096, 32, 8, 128, 14336, 2048)
 # query heads and 1 of the 8 KV heads (W_qkv 4096 x 768), the matching 512
 # rows of W_o, 1792 of the 14336 gate and up columns (W_gu 4096 x 3584) and
 # rows of W_down (1792 x 4096), the KV cache of its head [16, 1, 2048, 128].
-# The step computes exactly that shard's work; the two all-reduces of a
-# 16 x 4096 partial sum (after W_o and after W_down) are not part of it.
+# It is a cost proxy for one shard's work, not a usable shard: the step adds
+# the full residual and normalises its own partial x1, so the shards' outputs
+# do not all-reduce to the layer's (a real shard splits the step at W_o and
+# all-reduces between the halves).
 _decode_step("llama_decoder_step_tp8", 16, 4096, 4, 1, 128, 1792, 2048)
 
 # ---- LLaMA decoder layer, prefill, the reference's own shape (fp32) ------------

@@ -151,3 +151,92 @@ def test_profile_counter_parsing_and_absent_profiler(tmp_path, monkeypatch):
     monkeypatch.setattr(shutil, "which", lambda name: None)
     prof = harness.profile_counters("sqr_mm", 0)
     assert prof["counters_available"] is False and "rocprofv3" in prof["reason"]
+
+
+def test_cli_xcode_flags_reach_the_manifest():
+    """--xcode / --gputracer / --capture-host parse as in the reference
+    (mlx/scripts/harness.py:395-400) and put `capture_path` in the manifest
+    (mlx_helpers.py:333-334); --dry-run makes no GPU call."""
+    for flag in ("--xcode", "--gputracer"):
+        r = subprocess.run([sys.executable, "mlx/scripts/harness.py", "sqr_mm", flag, "--dry-run"],
+                           cwd=REPO, capture_output=True, text=True, timeout=120)
+        assert r.returncode == 0, r.stderr
+        m = json.loads(r.stdout)
+        assert m["capture_path"].endswith("/sqr_mm.trace")
+        assert "[xcode] will record a kernel trace" in r.stderr
+    r = subprocess.run([sys.executable, "mlx/scripts/harness.py", "transpose_2d", "--dry-run",
+                        "--capture-host", "/tmp/mb_cap"], cwd=REPO, capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert json.loads(r.stdout)["capture_path"] == "/tmp/mb_cap"
+    r = subprocess.run([sys.executable, "mlx/scripts/harness.py", "transpose_2d", "--dry-run"],
+                       cwd=REPO, capture_output=True, text=True, timeout=120)
+    assert "capture_path" not in json.loads(r.stdout)
+
+
+def test_kernel_trace_parsing_and_absent_profiler(tmp_path, monkeypatch):
+    csv_path = tmp_path / "x_kernel_trace.csv"
+    csv_path.write_text(
+        '"Kind","Dispatch_Id","Kernel_Name","Start_Timestamp","End_Timestamp"\n'
+        '"KERNEL_DISPATCH",3,"mb::(anonymous namespace)::attention_kernel<4>(mb::AttnArgs)",100,2600\n'
+        '"KERNEL_DISPATCH",1,"void at::native::vectorized_elementwise_kernel<4>(int)",0,50\n'
+        '"KERNEL_DISPATCH",2,"mb::(anonymous namespace)::qkv_kernel(mb::QkvArgs)",60,90\n')
+    got = harness.parse_kernel_trace_csv(csv_path)
+    assert [k["duration_ns"] for k in got] == [30, 2500]     # dispatch order, torch's excluded
+    assert "qkv_kernel" in got[0]["name"]
+    import shutil
+    monkeypatch.setattr(shutil, "which", lambda name: None)
+    cap = harness.capture_dispatch("sqr_mm", 0, tmp_path / "t.trace")
+    assert cap["written"] is False and "rocprofv3" in cap["reason"]
+    assert harness.available_counter_sets() == []
+
+
+def test_report_prints_counter_sets_and_trace():
+    res = _fake_result()
+    res["available_counter_sets"] = ["GRBM_GUI_ACTIVE", "FETCH_SIZE"]
+    res["capture"] = {"written": True, "path": "/x/transpose_2d.trace",
+                      "kernels": [{"name": "mb::(anonymous namespace)::transpose_kernel(float const*)",
+                                   "duration_ns": 93100}]}
+    buf = io.StringIO()
+    with redirect_stdout(buf):
+        harness._print_report(res, "speed", 1.0)
+    out = buf.getvalue()
+    # the reference prints the counter sets right after the occupancy line (harness.py:295-297)
+    lines = out.splitlines()
+    i = next(n for n, l in enumerate(lines) if l.startswith("  occupancy   :"))
+    assert lines[i + 1] == "  counters    : GRBM_GUI_ACTIVE, FETCH_SIZE"
+    assert "  trace       : /x/transpose_2d.trace" in out
+    assert re.search(r"transpose_kernel\s+93\.1 µs", out)
+
+
+def test_bench_script_dispatches_gputracer(tmp_path):
+    """`./bench --gputracer <name>` and `./bench <name> --xcode` reach the
+    harness with --xcode, and `--gputracer --all` walks every registry set
+    (reference bench:17-40).  A stub python3 on PATH records the calls."""
+    stub = tmp_path / "python3"
+    log = tmp_path / "calls"
+    stub.write_text(f"""#!/bin/bash
+if [ "$1" = "-c" ]; then exec {sys.executable} "$@"; fi
+echo "$*" >> {log}
+echo "[host] trace written: /x"
+""")
+    stub.chmod(0o755)
+    import os
+    env = dict(os.environ, SKIP_BUILD="1", PATH=f"{tmp_path}:{os.environ['PATH']}")
+    for argv in (["--gputracer", "conv2d"], ["conv2d", "--xcode"], ["conv2d", "--gputracer"]):
+        log.write_text("")
+        r = subprocess.run(["./bench", *argv], cwd=REPO, capture_output=True, text=True,
+                           timeout=60, env=env)
+        assert r.returncode == 0, r.stderr
+        call = log.read_text().split()
+        assert call[:2] == ["mlx/scripts/harness.py", "conv2d"] and "--xcode" in call, call
+        assert "--save" not in call
+    log.write_text("")
+    r = subprocess.run(["./bench", "--gputracer", "--all"], cwd=REPO, capture_output=True,
+                       text=True, timeout=120, env=env)
+    assert r.returncode == 0, r.stderr
+    calls = [c.split() for c in log.read_text().splitlines()]
+    names = {c[1] for c in calls}
+    assert {"sqr_mm", "transpose_2d", "conv2d", "large_mm", "llama_decoder_step"} <= names
+    assert all(c[2:4] == ["--xcode", "--metal-only"] for c in calls)
+    assert r.stdout.count("trace written") == len(calls)
