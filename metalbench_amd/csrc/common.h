@@ -169,6 +169,26 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Tile (tm, tn) of hardware block b in a tiles_m x tiles_n grid, XCD-aware.
+// The hardware dispatches block b to XCD b % 8, and each XCD has its own L2.
+// When the grid is a multiple of 8, each XCD takes a contiguous range of
+// logical tiles; logical tiles walk bands of `band` tile-rows in column order.
+// The tiles one XCD runs at a time then share `band` A panels and few B
+// panels in its L2.
+__device__ __forceinline__ void xcd_band_tile(uint32_t b, uint32_t nblocks, uint32_t tiles_m,
+                                              uint32_t tiles_n, uint32_t band, uint32_t* tm,
+                                              uint32_t* tn) {
+    uint32_t L = b;
+    if ((nblocks & 7) == 0) L = (b & 7) * (nblocks >> 3) + (b >> 3);
+    const uint32_t per_group = band * tiles_n;
+    const uint32_t group = L / per_group;
+    const uint32_t first_m = group * band;
+    const uint32_t gsize = min(tiles_m - first_m, band);
+    const uint32_t in_group = L - group * per_group;
+    *tm = first_m + in_group % gsize;
+    *tn = in_group / gsize;
+}
+
 // LDS address of a __shared__ object.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const lds_void_t*)p;

@@ -41,6 +41,8 @@ namespace mb {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -60,17 +62,7 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
 
 __device__ __forceinline__ void tile_coords(uint32_t b, uint32_t nblocks, uint32_t tiles_m,
                                             uint32_t tiles_n, uint32_t* tm, uint32_t* tn) {
-    // Hardware block b runs on XCD b % 8: give each XCD a contiguous range of
-    // logical tiles, then walk GM-row bands in column order.
-    uint32_t L = b;
-    if ((nblocks & 7) == 0) L = (b & 7) * (nblocks >> 3) + (b >> 3);
-    const uint32_t per_group = GM * tiles_n;
-    const uint32_t group = L / per_group;
-    const uint32_t first_m = group * GM;
-    const uint32_t gsize = min(tiles_m - first_m, (uint32_t)GM);
-    const uint32_t in_group = L - group * per_group;
-    *tm = first_m + in_group % gsize;
-    *tn = in_group / gsize;
+    xcd_band_tile(b, nblocks, tiles_m, tiles_n, GM, tm, tn);
 }
 
 template <int MODE>
@@ -364,10 +356,15 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
     // reads); the one hazard it cannot see -- reading an accumulator right
     // after the MFMA that writes it -- is padded before the epilogue.
     // Consecutive MFMAs share an operand register (snake order over j).
+    // The B fragment goes in the MFMA's first operand and the A fragment in
+    // its second, so the MFMA computes the 16x16 block transposed: lane l,
+    // register r of acc[i][j] is C row 16 i + l%16, column 16 j + 4 (l/16) + r
+    // (four consecutive columns of one row, which the epilogue packs into
+    // one 8-byte LDS write).  The products and their k order are the same.
     auto mfma = [&](int c, int i, int jj) {
         const int j = (i & 1) ? 7 - jj : jj;
         asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
-                     : "+a"(acc[i][j]) : "v"(a[c][i]), "v"(b[c][j]));
+                     : "+a"(acc[i][j]) : "v"(b[c][j]), "v"(a[c][i]));
     };
     // Stage s at unrolled position u = s % 4.  A pair q occupies slot q % 3
     // and is fetched a quarter per stage over stages 2q - 5 and 2q - 4, i.e.
@@ -460,19 +457,29 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
     asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory");
 
     // Epilogue through LDS (32 KB per wave: the three A slots and the first
-    // two B slots): lane l, reg r of 16x16 block (i, j) is row 16 i + 4 (l/16)
-    // + r, column 16 j + l%16 of the wave's 128 x 128 tile.
+    // two B slots, 128 rows of 256 B): lane l holds, for block (i, j), row
+    // 16 i + l%16, columns 16 j + 4 (l/16) .. +3, written as one packed 8-byte
+    // LDS store (the first version wrote 2-byte elements from the
+    // untransposed layout: ~2.8 us per tile, LDS-instruction bound; a DPP
+    // exchange to 4-byte pairs still took 2.0 us, VALU bound).  The 8-byte
+    // chunk c of row r sits at c ^ 4 (r % 8): the 64 lanes of a write (16 rows
+    // x 4 chunks) then fill every bank twice, the fewest for 512 bytes, and
+    // 16-byte row chunks stay contiguous for the reads below.
     lds_barrier();
-    uint16_t* ct = reinterpret_cast<uint16_t*>(wave < 3 ? AL + wave * A_SLOT_BYTES : BL);
+    uint8_t* ct = wave < 3 ? AL + wave * A_SLOT_BYTES : BL;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t row = 16 * i + t;
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t row = 16 * i + 4 * g + r;
-                ct[row * 128 + 16 * j + t] = __builtin_bit_cast(uint16_t, (__bf16)acc[i][j][r]);
-            }
+        for (int j = 0; j < 8; ++j) {
+            const f32x4 v = acc[i][j];
+            const u32x2 w = {
+                __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{v[0], v[1]}, bf16x2)),
+                __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{v[2], v[3]}, bf16x2))};
+            const uint32_t c8 = (4 * j + g) ^ (4 * (row & 7));
+            *reinterpret_cast<u32x2*>(ct + row * 256 + 8 * c8) = w;
+        }
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
@@ -482,7 +489,8 @@ void gemm_bf16_full_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
 #pragma unroll
     for (int q = 0; q < 32; ++q) {
         const uint32_t row = 4 * q + (lane >> 4), ch = lane & 15;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(ct + row * 128 + 8 * ch);
+        const u32x4 v = *reinterpret_cast<const u32x4*>(
+            ct + row * 256 + 16 * (ch ^ (2 * (row & 7))));
         __builtin_nontemporal_store(
             v, reinterpret_cast<u32x4*>(C + (size_t)(m0 + wm * 128 + row) * N + n0 + wn * 128 + 8 * ch));
     }

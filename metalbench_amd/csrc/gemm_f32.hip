@@ -253,6 +253,7 @@ void gemm_f32_kernel(GemmF32Args g) {
     }
 
     // 32x32 accumulator layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
+    // C is written once and not read here: non-temporal stores.
     const uint32_t gc = n0 + wn * 32 + li;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -292,7 +293,12 @@ void gemm_f32_kernel(GemmF32Args g) {
 //    barrier (every wave has read all of stage s; every wave's stage s+1 DMAs
 //    have landed), refills slot s % 4 with stage s+4 and reads stage s+1's
 //    first operands under group 3's MFMAs.
+//  * XCD-aware tile order (xcd_band_tile): at 1024^3 each XCD's 32 tiles are
+//    a band of DMA_BAND = 4 tile-rows by 8 tile-columns, which share 4 A and
+//    8 B panels in that XCD's L2 (in row-major order they shared 16 A and 2 B
+//    panels).
 constexpr int F_SLOT = BM * BK;              // floats per operand per stage slot (16 KB)
+constexpr uint32_t DMA_BAND = 4;
 
 __global__ __launch_bounds__(512)
 void gemm_f32_dma_kernel(GemmF32Args g) {
@@ -302,13 +308,12 @@ void gemm_f32_dma_kernel(GemmF32Args g) {
     const uint32_t lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wk = wave >> 2, wm = (wave >> 1) & 1, wn = wave & 1;
-    const uint32_t tm = blockIdx.x / g.tiles_n;
-    const uint32_t tn = blockIdx.x - tm * g.tiles_n;
+    uint32_t tm, tn;
+    xcd_band_tile(blockIdx.x, gridDim.x, gridDim.x / g.tiles_n, g.tiles_n, DMA_BAND, &tm, &tn);
     const uint32_t m0 = __builtin_amdgcn_readfirstlane(tm * BM);
     const uint32_t n0 = __builtin_amdgcn_readfirstlane(tn * BN);
     const uint32_t K = g.k, lda = g.lda, ldb = g.ldb;
     const uint32_t nstages = K / BK;   // a multiple of 4
-    const uint32_t last_k0 = K - BK;
     const float* A = g.a + (size_t)blockIdx.y * g.batch_a;
     const float* B = g.b + (size_t)blockIdx.y * g.batch_b;
     float* C = g.c + (size_t)blockIdx.y * g.batch_c;
@@ -355,8 +360,12 @@ void gemm_f32_dma_kernel(GemmF32Args g) {
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[c].z, b4[c].z, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[c].w, b4[c].w, acc, 0, 0, 0);
     };
-    auto stage = [&](auto slot_c, uint32_t s) {
+    // TAIL 0: a loop stage.  TAIL 1-3: the last four stages but one, which
+    // issue no DMA (every stage they need is requested) and so wait for
+    // 8, 4 and 0 DMA instructions.  TAIL 4: the last stage (no next stage).
+    auto stage = [&](auto slot_c, auto tail_c, uint32_t s) {
         constexpr int S = decltype(slot_c)::value;
+        constexpr int TAIL = decltype(tail_c)::value;
 #pragma unroll
         for (int gg = 0; gg < 3; ++gg) {
             __builtin_amdgcn_sched_barrier(0);
@@ -364,29 +373,43 @@ void gemm_f32_dma_kernel(GemmF32Args g) {
             mfma4(gg & 1);
             __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_s_waitcnt(0x0F78);   // vmcnt(8): stages s+2, s+3 may be in flight
-        lds_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-        dma(S, min((s + 4) * BK, last_k0));
-        read_ops((S + 1) & 3, 0, 0);
+        if constexpr (TAIL < 4) {
+            // vmcnt(8): stages s+2, s+3 may be in flight
+            if constexpr (TAIL <= 1) __builtin_amdgcn_s_waitcnt(0x0F78);
+            else if constexpr (TAIL == 2) __builtin_amdgcn_s_waitcnt(0x0F74);
+            else __builtin_amdgcn_s_waitcnt(0x0F70);
+            lds_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (TAIL == 0) dma(S, (s + 4) * BK);
+            read_ops((S + 1) & 3, 0, 0);
+        }
         mfma4(1);
         __builtin_amdgcn_sched_barrier(0);
     };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    using I4 = std::integral_constant<int, 4>;
 
 #pragma unroll
     for (int st = 0; st < 4; ++st) dma(st, st * BK);
     __builtin_amdgcn_s_waitcnt(0x0F7C);   // vmcnt(12): stage 0 has landed
     lds_barrier();
     read_ops(0, 0, 0);
-    // nstages % 4 == 0, so the body is straight-line; past the last stage the
-    // clamped DMAs re-read it into slots that are never read again.
-    for (uint32_t s = 0; s < nstages; s += 4) {
-        stage(std::integral_constant<int, 0>{}, s);
-        stage(std::integral_constant<int, 1>{}, s + 1);
-        stage(std::integral_constant<int, 2>{}, s + 2);
-        stage(std::integral_constant<int, 3>{}, s + 3);
+    // nstages % 4 == 0, so the body is straight-line; the last four stages
+    // are peeled: they request nothing, and every DMA has landed when the
+    // last one starts.
+    for (uint32_t s = 0; s + 4 < nstages; s += 4) {
+        stage(I0{}, I0{}, s);
+        stage(I1{}, I0{}, s + 1);
+        stage(I2{}, I0{}, s + 2);
+        stage(I3{}, I0{}, s + 3);
     }
-    __builtin_amdgcn_s_waitcnt(0);   // no DMA may still target LDS
+    stage(I0{}, I1{}, nstages - 4);
+    stage(I1{}, I2{}, nstages - 3);
+    stage(I2{}, I3{}, nstages - 2);
+    stage(I3{}, I4{}, nstages - 1);
     __syncthreads();
 
     // The second K half hands its partial sums to the first through LDS.
@@ -401,11 +424,12 @@ void gemm_f32_dma_kernel(GemmF32Args g) {
     for (int r = 0; r < 16; ++r) acc[r] += red[((wave & 3) * 16 + r) * 64 + lane];
 
     // 32x32 accumulator layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
+    // C is written once and not read here: non-temporal stores.
     const uint32_t gc = n0 + wn * 32 + li;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const uint32_t gr = m0 + wm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        C[(size_t)gr * g.ldc + gc] = acc[r];
+        __builtin_nontemporal_store(acc[r], &C[(size_t)gr * g.ldc + gc]);
     }
 }
 

@@ -58,15 +58,21 @@ def test_profile_sqr_mm_mfma_busy_cycles_closed_form():
 def test_profile_decoder_step_hbm_traffic():
     """The decode step streams 570,753,024 algorithmic bytes (weights, KV cache,
     x, y and the new k, v); the one profiled dispatch is the first of its
-    process, so L2 holds none of it and FETCH_SIZE (KiB of L2-miss reads) is
-    at least nearly all of it.  Writes are the new k, v and y plus workspace."""
+    process, so L2 holds none of it and its L2-miss reads are at least nearly
+    all of it.  On gfx950 FETCH_SIZE counts those reads at half their bytes:
+    a plain copy of 256 MiB reads 131,088 KiB (READ_SCALE 2, the calibration
+    bench.py --copy-calibration measures).  The step's workspace traffic (split-K
+    partials) and the prefetched weight units that later kernels fetch again
+    keep the total below 1.2x of the algorithmic bytes."""
+    READ_SCALE = 2.0
     r, out = _bench("llama_decoder_step", "--no-save", "--", "--no-session", "--profile",
                     "--iters", "3", "--warmup", "1", "--cpu-iters", "1")
     assert r.returncode == 0, out[-3000:]
     s = _samples(out)
-    fetch_bytes = s["FETCH_SIZE"] * 1024
-    assert 0.9 * 570_753_024 <= fetch_bytes <= 4 * 570_753_024, s
-    assert s["WRITE_SIZE"] > 0, s
+    fetch_bytes = s["FETCH_SIZE"] * 1024 * READ_SCALE
+    assert 0.95 * 570_753_024 <= fetch_bytes <= 1.3 * 570_753_024, s
+    # y, k_new and v_new at least (WRITE_SIZE counts whole bytes)
+    assert s["WRITE_SIZE"] * 1024 >= 2 * (16 * 4096 + 2 * 16 * 8 * 128), s
 
 
 def test_xcode_trace_of_decoder_step_names_its_five_kernels():
