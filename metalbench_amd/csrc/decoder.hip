@@ -804,9 +804,11 @@ void attention_kernel(StepParams p) {
     load_xs(0);
     load_item(base0, n0, 0);
     const f32x4 rope0 = *reinterpret_cast<const f32x4*>(p.rope + 4 * (item0 % (DH / 4)));
+    // Both slots of the ring are filled before the prologue's arithmetic,
+    // so 2 x 32 KB per workgroup stream while it waits for the partials.
     KVBlock kv[AR];
 #pragma unroll
-    for (int u = 0; u < AR - 1; ++u) {
+    for (int u = 0; u < AR; ++u) {
         load(kv[u], u);
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -924,18 +926,20 @@ void attention_kernel(StepParams p) {
         __builtin_amdgcn_wave_barrier();
     };
 
-    // A ring of AR blocks: block t + AR - 1 is issued right before block t is
-    // computed, so AR blocks (AR x 32 KB per workgroup) are in flight.  Four
-    // in flight measured 1.5 us slower than two at the benchmark shape (more
-    // concurrent streams per CU, less DRAM page locality).  sched_barrier
-    // pins the order.
+    // A ring of AR blocks: block t + AR goes into block t's slot as soon as
+    // block t is computed, so while block t + 1 is computed block t + 2 is in
+    // flight (AR = 2), as when block t + AR - 1 was issued right before block
+    // t; only the start differs (both slots already in flight during the
+    // prologue).  Four in flight measured 1.5 us slower than two at the
+    // benchmark shape (more concurrent streams per CU, less DRAM page
+    // locality).  sched_barrier pins the order.
     for (uint32_t t = 0; t < nblk; t += AR) {
 #pragma unroll
         for (int u = 0; u < AR; ++u) {
             __builtin_amdgcn_sched_barrier(0);
-            load(kv[(u + AR - 1) % AR], t + u + AR - 1);
-            __builtin_amdgcn_sched_barrier(0);
             compute(kv[u], t + u);
+            __builtin_amdgcn_sched_barrier(0);
+            load(kv[u], t + u + AR);
         }
     }
 
@@ -1176,7 +1180,7 @@ static int make_plan(const mb_decoder_step_args* a, Plan* pl) {
         const uint32_t per = cdiv(std::max(a->cache_len, 1u), std::min(want, nmax));
         pl->split_keys = cdiv(per, AR * AKEYS) * AR * AKEYS;
         pl->nsplit = std::max(1u, cdiv(a->cache_len, pl->split_keys));
-        // the ring's loads run up to AR - 1 blocks past the split
+        // the ring's loads run up to AR blocks past the split
         if ((uint64_t)(pl->split_keys + AR * AKEYS) * DH * 2 > 0xffffffffull)
             return fail(MB_E_ARG, "decoder step: cache_len %u too large", a->cache_len);
     }
