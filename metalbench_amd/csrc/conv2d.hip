@@ -41,7 +41,15 @@ struct ConvShape {
     uint32_t n, h, w, c, o, r, s, stride, pad, p, q;
     uint32_t m;   // n*p*q
     uint32_t k;   // r*s*c
+    uint32_t q_mul, q_sh, p_mul, p_sh;   // x / q and x / p for x < 2^31 (mul 0: divisor 1)
 };
+
+// floor(x / d) for x < 2^31 from (mul, sh) = magic_u31(d) (launch_conv2d).
+// The DMA kernel divides pixel indices below M, and its path requires
+// M O 4 < 2^31.
+__device__ __forceinline__ uint32_t div_magic(uint32_t x, uint32_t mul, uint32_t sh) {
+    return mul ? __umulhi(x, mul) >> sh : x;
+}
 
 template <int KSPLIT>
 __global__ __launch_bounds__(256 * KSPLIT)
@@ -263,8 +271,10 @@ void conv2d_f32_dma_kernel(const float* __restrict__ X, const float* __restrict_
     const uint32_t m = m0 + drow;
     const bool m_ok = m < sh.m;
     const uint32_t mm = m_ok ? m : 0;
-    const uint32_t qq = mm % sh.q, t = mm / sh.q;
-    const uint32_t pp = t % sh.p, nn = t / sh.p;
+    // (multiply-high divisions: the compiler's 32-bit divide is ~20 VALU
+    // instructions, and this set-up runs beside other workgroups' MFMA loops)
+    const uint32_t t = div_magic(mm, sh.q_mul, sh.q_sh), qq = mm - t * sh.q;
+    const uint32_t nn = div_magic(t, sh.p_mul, sh.p_sh), pp = t - nn * sh.p;
     const int32_t h0 = (int32_t)(pp * sh.stride) - (int32_t)sh.pad;
     const int32_t w0 = (int32_t)(qq * sh.stride) - (int32_t)sh.pad;
     const uint32_t xbase = (nn * sh.h * sh.w * sh.c + 4 * dch) * 4;   // bytes
@@ -374,12 +384,22 @@ void conv2d_f32_dma_kernel(const float* __restrict__ X, const float* __restrict_
     for (int r = 0; r < 16; ++r) acc[r] += red[(rw * 16 + r) * 64 + lane];
 
     // 32x32 accumulator: lane l, reg r -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
+    // Buffer stores through a descriptor clipped to the output: rows past M
+    // fall outside it, columns past O take an out-of-range offset.  One
+    // 32-bit add per store instead of a guarded 64-bit address: this
+    // epilogue runs beside five other workgroups' MFMA loops, where every
+    // VALU instruction waits for an issue slot (3.9-4.3 us per tile with the
+    // guarded stores, stamped).
     const uint32_t gc = n0 + wn * 32 + li;
+    const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc(
+        Y, 0, __builtin_amdgcn_readfirstlane(sh.m * sh.o * 4), 0x00020000);
+    const uint32_t ybase = gc < sh.o ? ((m0 + wm * 32 + 4 * lh) * sh.o + gc) * 4 : 0x80000000u;
+    const uint32_t o4 = sh.o * 4;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const uint32_t gr = m0 + wm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        if (gr < sh.m && gc < sh.o) Y[(uint64_t)gr * sh.o + gc] = acc[r];
-    }
+    for (int r = 0; r < 16; ++r)   // (not __builtin_bit_cast(uint32_t, acc[r]): hipcc
+                                   // compiled that as a read of element 0)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[r]), yrs,
+                                              ybase + (8 * (r >> 2) + (r & 3)) * o4, 0, 0);
 }
 
 int launch_conv2d(const float* x, const float* w, float* y, uint32_t n, uint32_t h, uint32_t wd,
@@ -401,15 +421,28 @@ int launch_conv2d(const float* x, const float* w, float* y, uint32_t n, uint32_t
         return fail(MB_E_ARG, "conv2d_f32: shape too large");
     sh.m = (uint32_t)m;
     sh.k = (uint32_t)k;
+    // floor(x / d) = umulhi(x, M) >> (s - 1) for x < 2^31, with s = ceil(log2 d)
+    // and M = floor(2^(31+s) / d) + 1 < 2^32: M d - 2^(31+s) lies in (0, d],
+    // so x (M d - 2^(31+s)) < 2^31 d <= 2^(31+s) and the error stays below
+    // one step.  d = 1 takes the plain path (mul 0).
+    auto magic_u31 = [](uint32_t d, uint32_t* mul, uint32_t* shift) {
+        if (d <= 1) { *mul = 0; *shift = 0; return; }
+        uint32_t l = 0;
+        while ((1ull << l) < d) ++l;
+        *mul = (uint32_t)(((1ull << (31 + l)) / d) + 1);
+        *shift = l - 1;
+    };
+    magic_u31(sh.q, &sh.q_mul, &sh.q_sh);
+    magic_u31(sh.p, &sh.p_mul, &sh.p_sh);
     if (sh.m == 0 || o == 0) return MB_OK;
     const uint32_t tiles_m = cdiv(sh.m, BM), tiles_n = cdiv(o, BN);
     const uint64_t nblocks = (uint64_t)tiles_m * tiles_n;
     if (nblocks > 0x7fffffffull) return fail(MB_E_ARG, "conv2d_f32: shape too large");
-    // fast path: a stage never straddles a tap, 16-byte aligned rows, and DMA
-    // offsets of both operands within 2 GB
+    // fast path: a stage never straddles a tap, 16-byte aligned rows, and
+    // buffer offsets of both operands and of the output within 2 GB
     const bool fast = (c % BK == 0) && ((((uintptr_t)x) | ((uintptr_t)w)) & 15) == 0 &&
                       (uint64_t)n * h * wd * c * 4 < 0x80000000ull &&
-                      (uint64_t)o * k * 4 < 0x80000000ull;
+                      (uint64_t)o * k * 4 < 0x80000000ull && (uint64_t)sh.m * o * 4 < 0x80000000ull;
     if (fast) {
         const uint64_t dma_blocks = (uint64_t)cdiv(sh.m, 32) * tiles_n;
         if (dma_blocks > 0x7fffffffull) return fail(MB_E_ARG, "conv2d_f32: shape too large");
