@@ -270,10 +270,10 @@ void gemm_f32_kernel(GemmF32Args g) {
     }
 }
 
-// Full-tile kernel for C = A B: M, N multiples of 64, K a multiple of 256 and
-// at least 512, B [K][N], 16-byte aligned rows, operands under 2 GB.  Same
-// tile, waves and MFMA as
-// gemm_f32_kernel<2, true, BL_KN, EPI_STORE, false>, but the operands go
+// Full-tile kernel for C = A B or rmsnorm(A) B: M, N multiples of 64, K a
+// multiple of 256 and at least 512, B [K][N] or [N][K] (BL), 16-byte aligned
+// rows, operands under 2 GB.  Same tile, waves and MFMA as
+// gemm_f32_kernel<2, true, BL, EPI_STORE, RMS>, but the operands go
 // global -> LDS by DMA (buffer_load ... lds) into a ring of four 64-deep k
 // stages (A 16 KB + B 16 KB each): no staging registers and no LDS store
 // instructions, whose VGPR reads held the MFMA pipe to ~72 % busy (~91 %
@@ -297,12 +297,21 @@ void gemm_f32_kernel(GemmF32Args g) {
 //    a band of DMA_BAND = 4 tile-rows by 8 tile-columns, which share 4 A and
 //    8 B panels in that XCD's L2 (in row-major order they shared 16 A and 2 B
 //    panels).
+//  * BL_NK (B given as [N][K], rms_norm_linear's W): the B slot holds 64
+//    K-contiguous n-rows exactly as the A slot holds m-rows (same swizzle,
+//    same DMA pattern), and the MFMA B operand is read like the A operand;
+//  * RMS (C = rmsnorm(A) B): every A element passes through the waves with
+//    wn = 0 exactly once, as an MFMA operand, so they square-sum it there;
+//    the row sums meet in LDS after the loop and scale C's rows by
+//    rsqrt(sum / K + eps) before the store.
 constexpr int F_SLOT = BM * BK;              // floats per operand per stage slot (16 KB)
 constexpr uint32_t DMA_BAND = 4;
 
+template <int BL, bool RMS>
 __global__ __launch_bounds__(512)
 void gemm_f32_dma_kernel(GemmF32Args g) {
     __shared__ __attribute__((aligned(1024))) float L[4][2 * F_SLOT];
+    __shared__ float row_ss[2][BM];   // RMS: per K half, each A row's sum of squares
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63;
@@ -318,14 +327,16 @@ void gemm_f32_dma_kernel(GemmF32Args g) {
     const float* B = g.b + (size_t)blockIdx.y * g.batch_b;
     float* C = g.c + (size_t)blockIdx.y * g.batch_c;
 
-    const i32x4 ars = dma_rsrc(A, g.m * lda * 4), brs = dma_rsrc(B, K * ldb * 4);
-    // DMA instruction i (0, 1) of wave w: rows (A) / k-rows (B) 8 w + 4 i + l/16, slot l%16.
+    constexpr bool BT = BL == BL_NK;
+    const i32x4 ars = dma_rsrc(A, g.m * lda * 4), brs = dma_rsrc(B, (BT ? g.n : K) * ldb * 4);
+    // DMA instruction i (0, 1) of wave w: rows (A, B^T) / k-rows (B) 8 w + 4 i + l/16, slot l%16.
     const uint32_t r4 = lane >> 4, sl = lane & 15;
     uint32_t a_voff[2], b_voff[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         a_voff[i] = (r4 * lda + 4 * (sl ^ ((8 * (wave & 1) + 4 * i + r4) & 15))) * 4;
-        b_voff[i] = (r4 * ldb + 4 * (sl ^ (8 * i))) * 4;
+        b_voff[i] = BT ? (r4 * ldb + 4 * (sl ^ ((8 * (wave & 1) + 4 * i + r4) & 15))) * 4
+                       : (r4 * ldb + 4 * (sl ^ (8 * i))) * 4;
     }
     const uint32_t l0 = lds_addr(&L[0][0]);
     auto dma = [&](int slot, uint32_t k0) {
@@ -334,7 +345,7 @@ void gemm_f32_dma_kernel(GemmF32Args g) {
             const uint32_t r = 8 * wave + 4 * i;
             dma16(ars, l0 + slot * (8 * F_SLOT) + r * 256, a_voff[i], ((m0 + r) * lda + k0) * 4);
             dma16(brs, l0 + slot * (8 * F_SLOT) + 4 * F_SLOT + r * 256, b_voff[i],
-                  ((k0 + r) * ldb + n0) * 4);
+                  BT ? ((n0 + r) * ldb + k0) * 4 : ((k0 + r) * ldb + n0) * 4);
         }
     };
 
@@ -344,17 +355,30 @@ void gemm_f32_dma_kernel(GemmF32Args g) {
     // B operand of group gi, t = 0..3: k-row 8 gi + 4 lh + t, column wn*32 + li
     // (chunk wn*8 + li/4 ^ 8 lh, float li % 4).
     const uint32_t b_col = 16 * ((wn * 8 + (li >> 2)) ^ (8 * lh)) + 4 * (li & 3) + 4 * lh * 256;
+    // B^T operand of group gi: n-row wn*32 + li, chunk 2 gi + lh, swizzled as A's.
+    const uint32_t bt_row = 4 * F_SLOT + (wn * 32 + li) * 256;
     const uint8_t* l8 = reinterpret_cast<const uint8_t*>(&L[0][0]);
     float4 a4[2], b4[2];
     auto read_ops = [&](int slot, int gg, int c) {
         const int gi = (int)wk * 4 + gg;
         const uint8_t* base = l8 + slot * (8 * F_SLOT);
         a4[c] = *reinterpret_cast<const float4*>(base + a_row + 16 * ((2 * gi + lh) ^ a_sw));
-        const float* bp = reinterpret_cast<const float*>(base + 4 * F_SLOT + 8 * gi * 256 + b_col);
-        b4[c] = make_float4(bp[0], bp[64], bp[128], bp[192]);
+        if (BT) {
+            b4[c] = *reinterpret_cast<const float4*>(base + bt_row + 16 * ((2 * gi + lh) ^ a_sw));
+        } else {
+            const float* bp = reinterpret_cast<const float*>(base + 4 * F_SLOT + 8 * gi * 256 + b_col);
+            b4[c] = make_float4(bp[0], bp[64], bp[128], bp[192]);
+        }
     };
     f32x16 acc = f32x16{};
+    float ss = 0.f;   // RMS: this lane's share of its A row's sum of squares
     auto mfma4 = [&](int c) {
+        if (RMS) {
+            ss = fmaf(a4[c].x, a4[c].x, ss);
+            ss = fmaf(a4[c].y, a4[c].y, ss);
+            ss = fmaf(a4[c].z, a4[c].z, ss);
+            ss = fmaf(a4[c].w, a4[c].w, ss);
+        }
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[c].x, b4[c].x, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[c].y, b4[c].y, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[c].z, b4[c].z, acc, 0, 0, 0);
@@ -418,10 +442,21 @@ void gemm_f32_dma_kernel(GemmF32Args g) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) red[((wave & 3) * 16 + r) * 64 + lane] = acc[r];
     }
+    if (RMS) {   // lanes li and li + 32 read row wm*32 + li's two chunks of each group
+        ss += __shfl_xor(ss, 32);
+        if (wn == 0 && lh == 0) row_ss[wk][wm * 32 + li] = ss;
+    }
     __syncthreads();
     if (wk == 1) return;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] += red[((wave & 3) * 16 + r) * 64 + lane];
+    if (RMS) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t lr = wm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+            acc[r] *= rsqrtf((row_ss[0][lr] + row_ss[1][lr]) / (float)K + g.eps);
+        }
+    }
 
     // 32x32 accumulator layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
     // C is written once and not read here: non-temporal stores.
@@ -448,15 +483,17 @@ int launch_variant(const GemmF32Args& g, uint32_t batch, hipStream_t s) {
                      (uint64_t)g.m * g.lda * 4 < 0x80000000ull &&
                      b_rows * g.ldb * 4 < 0x80000000ull;
     const dim3 grid((uint32_t)nblocks, batch), block(512);
-    // full tiles of the plain product (sqr_mm, rect_mm, fused_qkv_projection)
-    // take the DMA kernel when K is long enough for its ring to pay: at K = 256
+    // full tiles of the plain and RMS products (sqr_mm, rect_mm,
+    // fused_qkv_projection, rms_norm_linear) take the DMA kernel when K is
+    // long enough for its ring to pay: at K = 256
     // (batch_mm's 128 x (128x512x256)) its 128 KB of LDS (one workgroup per
     // CU) made it 4-5 % slower than the register-staged kernel
-    if (BL == BL_KN && !RMS && EPI == EPI_STORE && vec && g.m % BM == 0 && g.n % BN == 0 &&
-        g.k % (4 * BK) == 0 && g.k >= 8 * BK) {
-        hipLaunchKernelGGL(gemm_f32_dma_kernel, grid, block, 0, s, g);
-        MB_LAUNCH_CHECK("matmul_f32");
-        return MB_OK;
+    if constexpr (EPI == EPI_STORE && (!RMS || BL == BL_NK)) {
+        if (vec && g.m % BM == 0 && g.n % BN == 0 && g.k % (4 * BK) == 0 && g.k >= 8 * BK) {
+            hipLaunchKernelGGL((gemm_f32_dma_kernel<BL, RMS>), grid, block, 0, s, g);
+            MB_LAUNCH_CHECK("matmul_f32");
+            return MB_OK;
+        }
     }
     if (vec) hipLaunchKernelGGL((gemm_f32_kernel<2, true, BL, EPI, RMS>), grid, block, 0, s, g);
     else hipLaunchKernelGGL((gemm_f32_kernel<2, false, BL, EPI, RMS>), grid, block, 0, s, g);
@@ -587,14 +624,14 @@ void register_gemm_f32() {
     // sqr_mm, rect_mm and fused_qkv_projection share the plain GEMM's spec;
     // their registry shapes run the LDS-DMA kernel, whose attributes (LDS
     // size, threads) the report prints.
-    const void* dma = reinterpret_cast<const void*>(&gemm_f32_dma_kernel);
+    const void* dma = reinterpret_cast<const void*>(&gemm_f32_dma_kernel<BL_KN, false>);
     register_kernel({"sqr_matmul_f32", run_gemm_f32, dma, 1});
     register_kernel({"rect_matmul_f32", run_gemm_f32, dma, 1});
     register_kernel({"fused_qkv_projection_f32", run_gemm_f32, dma, 1});
     register_kernel({"batch_matmul_f32", run_batch_mm, plain, 1});
+    // (rms_norm_linear's registry shape, 1024^3, takes the LDS-DMA kernel)
     register_kernel({"rms_norm_linear_f32", run_rms_norm_linear,
-                     reinterpret_cast<const void*>(&gemm_f32_kernel<2, true, BL_NK, EPI_STORE, true>),
-                     1});
+                     reinterpret_cast<const void*>(&gemm_f32_dma_kernel<BL_NK, true>), 1});
     register_kernel({"swiglu_f32", run_swiglu,
                      reinterpret_cast<const void*>(&gemm_f32_kernel<2, true, BL_KN, EPI_SWIGLU, false>),
                      1});

@@ -85,7 +85,9 @@ def test_fused_add_rms_norm_shapes(mb, rows, cols):
                  f"fused_add_rms_norm {rows}x{cols}")
 
 
-@pytest.mark.parametrize("m,n,k", [(70, 90, 130), (64, 64, 64), (1, 3, 5)])
+@pytest.mark.parametrize("m,n,k", [(70, 90, 130), (64, 64, 64), (1, 3, 5),
+                                   # full 64-tiles, K a multiple of 256: the LDS-DMA kernel
+                                   (128, 192, 512), (64, 320, 768), (192, 64, 1024)])
 def test_rms_norm_linear_shapes(mb, m, n, k):
     x, w = seeded(4, (m, k)), seeded(5, (n, k))
     (y,) = run_bound("rms_norm_linear_f32", [(0, x), (1, w)], [(2, (m, n))],
