@@ -1,6 +1,8 @@
 // fp32 GEMM family on fp32 MFMA: C[M][N] = A[M][K] @ B (row-major), with
 // optional batching, a transposed B, an RMSNorm row scale and fused
-// epilogues.  One kernel template serves these registry entries:
+// epilogues.  Three kernels (register-staged 64 x 64 tiles for any shape,
+// LDS-DMA 64 x 64 tiles for full tiles and long K, and 32 x 32 tiles with
+// K spread over waves for small problems) serve these registry entries:
 //   sqr_mm, rect_mm, fused_qkv_projection   plain C = A B
 //     (reference mlx/kernels/common/sqr_mm.py:10-11, rect_mm.py:10-11,
 //      standard/fused_qkv_projection.py:12-13; registry common/registry.py:
@@ -468,6 +470,131 @@ void gemm_f32_dma_kernel(GemmF32Args g) {
     }
 }
 
+// Small problems (fewer 64 x 64 tiles than half the CUs, K <= 512: the
+// fused_qkv_projection and swiglu registry shapes, the prefill layer's and
+// llama_attention's projections).  There a 64 x 64 tile per workgroup leaves
+// most CUs idle while a few run the whole K loop.  Here a workgroup owns one
+// 32 x 32 output tile and spreads K over W = ceil(K / 32) waves (up to 16):
+// wave w loads its 32-deep slice with one round of buffer loads (A rows as
+// float4, B as float4 rows of [N][K] or as four k-rows of [K][N]; rows,
+// columns and k past the shape read zeros through out-of-range offsets),
+// runs 16 MFMAs (v_mfma_f32_32x32x2f32, the same k order as the 64 x 64
+// kernels: lane l holds k = 8 g + 4 (l / 32) + t of group g, MFMA t), and
+// leaves its partial tile in LDS.  The W partials are summed in wave order,
+// so the result does not depend on timing, and the epilogue (RMSNorm row
+// scale from the slices' sums of squares, residual, SwiGLU) runs on the sum.
+constexpr uint32_t SM_MAX_K = 512;   // 16 waves x 32 k
+
+template <int BL, int EPI, bool RMS>
+__global__ __launch_bounds__(1024)
+void gemm_f32_small_kernel(GemmF32Args g, uint32_t tiles_n32) {
+    constexpr bool DUAL = EPI == EPI_SWIGLU;
+    constexpr int NB = DUAL ? 2 : 1;
+    __shared__ float part[16][NB][16][64];   // wave, operand, accumulator register, lane
+    __shared__ float rss[16][32];            // RMS: wave, row
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t nw = blockDim.x >> 6;
+    const uint32_t li = lane & 31, lh = lane >> 5;
+    const uint32_t tm = blockIdx.x / tiles_n32, tn = blockIdx.x - tm * tiles_n32;
+    const uint32_t m0 = tm * 32, n0 = tn * 32;
+    const uint32_t M = g.m, N = g.n, K = g.k;
+    const float* A = g.a + (size_t)blockIdx.y * g.batch_a;
+    const float* Bp[2] = {g.b + (size_t)blockIdx.y * g.batch_b,
+                          (DUAL ? g.b2 : g.b) + (size_t)blockIdx.y * g.batch_b};
+    float* C = g.c + (size_t)blockIdx.y * g.batch_c;
+
+    const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(A), 0, __builtin_amdgcn_readfirstlane(M * g.lda * 4), 0x00020000u);
+    const uint32_t b_bytes = __builtin_amdgcn_readfirstlane((BL == BL_KN ? K : N) * g.ldb * 4);
+    __amdgpu_buffer_rsrc_t brs[NB];
+#pragma unroll
+    for (int o = 0; o < NB; ++o)
+        brs[o] = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Bp[o]), 0, b_bytes, 0x00020000u);
+
+    const uint32_t row = m0 + li, col = n0 + li;
+    float4 av[4];
+    float4 bv[NB][4];   // group gi: B[k + t][col] for MFMA t
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+        const uint32_t k = wave * 32 + 8 * gi + 4 * lh;   // K % 4 == 0: all or none of k .. k+3
+        const uint32_t aoff = (row < M && k < K) ? (row * g.lda + k) * 4 : 0x80000000u;
+        av[gi] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ars, aoff, 0, 0));
+#pragma unroll
+        for (int o = 0; o < NB; ++o) {
+            if (BL == BL_NK) {
+                const uint32_t boff = (col < N && k < K) ? (col * g.ldb + k) * 4 : 0x80000000u;
+                bv[o][gi] = __builtin_bit_cast(
+                    float4, __builtin_amdgcn_raw_buffer_load_b128(brs[o], boff, 0, 0));
+            } else {
+                float t4[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint32_t boff =
+                        (col < N && k + t < K) ? ((k + t) * g.ldb + col) * 4 : 0x80000000u;
+                    t4[t] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(brs[o], boff, 0, 0));
+                }
+                bv[o][gi] = make_float4(t4[0], t4[1], t4[2], t4[3]);
+            }
+        }
+    }
+    f32x16 acc[NB];
+#pragma unroll
+    for (int o = 0; o < NB; ++o) acc[o] = f32x16{};
+    float ss = 0.f;
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+#pragma unroll
+        for (int o = 0; o < NB; ++o) {
+            acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[gi].x, bv[o][gi].x, acc[o], 0, 0, 0);
+            acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[gi].y, bv[o][gi].y, acc[o], 0, 0, 0);
+            acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[gi].z, bv[o][gi].z, acc[o], 0, 0, 0);
+            acc[o] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[gi].w, bv[o][gi].w, acc[o], 0, 0, 0);
+        }
+        if (RMS) ss += av[gi].x * av[gi].x + av[gi].y * av[gi].y + av[gi].z * av[gi].z +
+                       av[gi].w * av[gi].w;
+    }
+#pragma unroll
+    for (int o = 0; o < NB; ++o)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part[wave][o][r][lane] = acc[o][r];
+    if (RMS) {   // lanes li and li + 32 hold the two halves of row li's slice
+        ss += __shfl_xor(ss, 32);
+        if (lh == 0) rss[wave][li] = ss;
+    }
+    __syncthreads();
+
+    // element e of the tile: accumulator register r = e / 64 of lane l = e % 64,
+    // i.e. row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32
+    const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(
+        C, 0, __builtin_amdgcn_readfirstlane(M * g.ldc * 4), 0x00020000u);
+    for (uint32_t e = tid; e < 1024; e += 64 * nw) {
+        const uint32_t r = e >> 6, l = e & 63;
+        const uint32_t lr = 8 * (r >> 2) + 4 * (l >> 5) + (r & 3), lc = l & 31;
+        float v[NB];
+#pragma unroll
+        for (int o = 0; o < NB; ++o) {
+            float t = 0.f;
+            for (uint32_t w = 0; w < nw; ++w) t += part[w][o][r][l];
+            v[o] = t;
+        }
+        float sc = 1.0f;
+        if (RMS) {
+            float t = 0.f;
+            for (uint32_t w = 0; w < nw; ++w) t += rss[w][lr];
+            sc = rsqrtf(t / (float)K + g.eps);
+        }
+        const uint32_t gr = m0 + lr, gc = n0 + lc;
+        float out;
+        if (EPI == EPI_SWIGLU) out = silu_f(v[0] * sc) * (v[NB - 1] * sc);
+        else if (EPI == EPI_RESID) out = v[0] * sc + (gr < M && gc < N ? g.r[(size_t)gr * g.ldr + gc] : 0.f);
+        else out = v[0] * sc;
+        const uint32_t coff = (gr < M && gc < N) ? (gr * g.ldc + gc) * 4 : 0x80000000u;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(out), crs, coff, 0, 0);
+    }
+}
+
 template <int BL, int EPI, bool RMS>
 int launch_variant(const GemmF32Args& g, uint32_t batch, hipStream_t s) {
     const uint64_t nblocks = (uint64_t)cdiv(g.m, BM) * g.tiles_n;
@@ -482,6 +609,15 @@ int launch_variant(const GemmF32Args& g, uint32_t batch, hipStream_t s) {
                      (g.batch_a % 4 == 0) && (g.batch_b % 4 == 0) &&
                      (uint64_t)g.m * g.lda * 4 < 0x80000000ull &&
                      b_rows * g.ldb * 4 < 0x80000000ull;
+    // few 64 x 64 tiles and a short K: 32 x 32 tiles with K spread over waves
+    if (vec && g.k > 0 && g.k <= SM_MAX_K && nblocks * batch < 128 &&
+        (uint64_t)g.m * g.ldc * 4 < 0x80000000ull) {
+        const uint32_t tn32 = cdiv(g.n, 32);
+        const dim3 sgrid(cdiv(g.m, 32) * tn32, batch), sblock(64 * cdiv(g.k, 32));
+        hipLaunchKernelGGL((gemm_f32_small_kernel<BL, EPI, RMS>), sgrid, sblock, 0, s, g, tn32);
+        MB_LAUNCH_CHECK("matmul_f32");
+        return MB_OK;
+    }
     const dim3 grid((uint32_t)nblocks, batch), block(512);
     // full tiles of the plain and RMS products (sqr_mm, rect_mm,
     // fused_qkv_projection, rms_norm_linear) take the DMA kernel when K is

@@ -15,9 +15,13 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize("m,n,k", [
     (1, 1, 1), (1, 64, 64), (64, 1, 64), (64, 64, 1), (64, 64, 64), (65, 33, 17),
     (128, 256, 64), (100, 300, 96), (257, 129, 200), (512, 512, 512), (31, 1000, 36),
-    # full tiles with K % 256 == 0 and K >= 512 take the LDS-DMA kernel: two loop
-    # trips, three trips
-    (64, 64, 512), (192, 128, 768),
+    # fewer than 128 64x64 tiles and K <= 512 take the small-problem kernel
+    # (32x32 tiles, K over up to 16 waves): K = 32 (one wave), 464 (15 waves,
+    # the last one's slice half past K), ragged M and N
+    (32, 96, 32), (96, 64, 464), (70, 130, 256),
+    # full tiles with K % 256 == 0 and K >= 512 (and, at K = 512, at least 128
+    # tiles) take the LDS-DMA kernel: two loop trips, three trips
+    (1024, 512, 512), (192, 128, 768),
 ])
 def test_matmul_f32_shapes(mb, dev, m, n, k):
     a = seeded(m * 1000 + k, (m, k), ("uniform", -1.0, 1.0))
@@ -31,7 +35,8 @@ def test_matmul_f32_shapes(mb, dev, m, n, k):
 
 def _random_f32_shapes(n, seed=72):
     """Seeded shapes: half ragged, half full 64 x 64 tiles with K a multiple of
-    256 from 512 (the LDS-DMA kernel)."""
+    256 from 512 (the LDS-DMA kernel from K = 768, the small-problem kernel at
+    K = 512 when there are fewer than 128 tiles)."""
     rng = np.random.default_rng(seed)
     out = []
     for i in range(n):
@@ -55,7 +60,8 @@ def test_matmul_f32_k0_gives_zeros(mb, dev):
     assert torch.all(d_c.cpu() == 0.0)
 
 
-@pytest.mark.parametrize("n", [192, 256])   # register-staged kernel, LDS-DMA kernel
+# small-problem kernel, register-staged kernel (ragged), LDS-DMA kernel
+@pytest.mark.parametrize("n", [192, 1000, 1024])
 def test_matmul_f32_identity_exact(mb, dev, n):
     a = seeded(3, (n, n))
     eye = torch.eye(n)
