@@ -154,57 +154,65 @@ struct AttnPrefillArgs {
     float base, scale;  // RoPE base; 1 / sqrt(Dh)
 };
 
-constexpr int QB = 64;   // queries per workgroup (and keys per LDS chunk)
+constexpr int QW = 16;   // queries per workgroup
+constexpr int KC = 64;   // keys per LDS chunk
 
 template <typename T> __device__ __forceinline__ T exp_t(T v);
 template <> __device__ __forceinline__ float exp_t<float>(float v) { return expf(v); }
 template <> __device__ __forceinline__ double exp_t<double>(double v) { return exp(v); }
 
-// Rotation of pair (2j, 2j+1) at position pos: angle pos * base^(-2j/Dh),
-// in fp64 (an fp32 angle is off by ~pos * 6e-8 rad).
-__device__ __forceinline__ void rope_cs(uint32_t pos, uint32_t pair, uint32_t dh, float base,
-                                        double* cs, double* sn) {
-    const double ang = (double)pos * pow((double)base, -2.0 * (double)pair / (double)dh);
-    *sn = sin(ang);
-    *cs = cos(ang);
-}
-
-// Workgroup (head h, 64 queries); lanes 4q .. 4q+3 own query q, DP = Dh/4
-// head dims each.  q and k are rotated by their positions (the row index)
-// with omega_j = base^(-2j/Dh) on interleaved pairs (2j, 2j+1).
-template <int DP, typename T>
+// Workgroup (head h, 16 queries); the 16 lanes 16 qq .. 16 qq + 15 of a wave
+// own query qq of the block.  Per chunk of 64 keys: the keys are rotated
+// into LDS (omega_j = base^(-2j/Dh) once per pair index, the angle pos *
+// omega_j and its sine and cosine in fp64: an fp32 angle is off by ~pos *
+// 6e-8 rad), lane kg of a query scores keys kg, kg + 16, kg + 32, kg + 48
+// (a Dh-long dot product each), the query's 16 lanes fold the chunk's
+// maximum and sum with shuffles (online softmax across chunks), write the
+// probabilities to LDS and update their Dh / 16 output dims over the
+// chunk's keys.  q and k are rotated by their positions (the row index) on
+// interleaved pairs (2j, 2j+1).  (The first version gave a workgroup 64
+// queries, four lanes per query and keys one at a time: at S = 64 that is
+// one workgroup per head and 64 dependent steps, 21 us for llama_attention's
+// registry shape.)
+template <int DH, typename T>
 __global__ __launch_bounds__(256)
 void attention_prefill_kernel(AttnPrefillArgs<T> a) {
-    constexpr int DH = 4 * DP;
-    __shared__ __attribute__((aligned(16))) T ks[QB][DH];
-    __shared__ __attribute__((aligned(16))) float vs[QB][DH];
+    constexpr int OD = DH / 16;   // output dims per lane
+    __shared__ T qs[QW][DH + 1];
+    __shared__ T ks[KC][DH + 1];
+    __shared__ float vs[KC][DH];
+    __shared__ T ps[QW][KC];
+    __shared__ double omega[DH / 2];
     const uint32_t tid = threadIdx.x;
     const uint32_t h = blockIdx.x, kvh = h / (a.H / a.Hkv);
-    const uint32_t qi = blockIdx.y * QB + tid / 4, part = tid % 4, d0 = part * DP;
+    const uint32_t q0 = blockIdx.y * QW;
+    const uint32_t qq = tid >> 4, kg = tid & 15;   // query of the block, lane within the query
     const uint32_t kcol = a.D + kvh * DH, vcol = a.D + a.Hkv * DH + kvh * DH;
 
-    T q[DP];
-#pragma unroll
-    for (int j = 0; j < DP / 2; ++j) {
+    if (tid < DH / 2) omega[tid] = pow((double)a.base, -2.0 * (double)tid / (double)DH);
+    __syncthreads();
+    for (uint32_t e = tid; e < QW * DH / 2; e += 256) {
+        const uint32_t i = e / (DH / 2), pair = e % (DH / 2), pos = q0 + i;
         T x0 = 0, x1 = 0;
-        if (qi < a.S) {
-            const T* src = a.qkv + (size_t)qi * a.ldq + h * DH + d0 + 2 * j;
+        if (pos < a.S) {
+            const T* src = a.qkv + (size_t)pos * a.ldq + h * DH + 2 * pair;
             x0 = src[0]; x1 = src[1];
         }
-        double cs, sn;
-        rope_cs(qi, d0 / 2 + j, DH, a.base, &cs, &sn);
-        q[2 * j] = x0 * (T)cs - x1 * (T)sn;
-        q[2 * j + 1] = x0 * (T)sn + x1 * (T)cs;
+        double sn, cs;
+        sincos((double)pos * omega[pair], &sn, &cs);
+        qs[i][2 * pair] = x0 * (T)cs - x1 * (T)sn;
+        qs[i][2 * pair + 1] = x0 * (T)sn + x1 * (T)cs;
     }
 
     T m_run = (T)NEG_BIG, l_run = 0;
-    T o[DP];
+    T o[OD];
 #pragma unroll
-    for (int d = 0; d < DP; ++d) o[d] = 0;
+    for (int d = 0; d < OD; ++d) o[d] = 0;
+    const uint32_t od = kg * OD;
 
-    for (uint32_t kc = 0; kc < a.S; kc += QB) {
-        __syncthreads();   // the previous chunk is no longer read
-        for (uint32_t e = tid; e < QB * DH / 2; e += 256) {
+    for (uint32_t kc = 0; kc < a.S; kc += KC) {
+        __syncthreads();   // q is written; the previous chunk is no longer read
+        for (uint32_t e = tid; e < KC * DH / 2; e += 256) {
             const uint32_t key = e / (DH / 2), pair = e % (DH / 2), kk = kc + key;
             T k0 = 0, k1 = 0, v0 = 0, v1 = 0;
             if (kk < a.S) {
@@ -212,35 +220,60 @@ void attention_prefill_kernel(AttnPrefillArgs<T> a) {
                 const T* vr = a.qkv + (size_t)kk * a.ldq + vcol + 2 * pair;
                 k0 = kr[0]; k1 = kr[1]; v0 = vr[0]; v1 = vr[1];
             }
-            double cs, sn;
-            rope_cs(kk, pair, DH, a.base, &cs, &sn);
+            double sn, cs;
+            sincos((double)kk * omega[pair], &sn, &cs);
             ks[key][2 * pair] = k0 * (T)cs - k1 * (T)sn;
             ks[key][2 * pair + 1] = k0 * (T)sn + k1 * (T)cs;
             vs[key][2 * pair] = (float)v0;
             vs[key][2 * pair + 1] = (float)v1;
         }
         __syncthreads();
-        const uint32_t nk = min((uint32_t)QB, a.S - kc);
+        const uint32_t nk = min((uint32_t)KC, a.S - kc);
+        T sc[4];
+        T cmax = (T)NEG_BIG;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t key = kg + 16 * i;
+            T dp[4] = {0, 0, 0, 0};   // four interleaved partial sums, added pairwise
+#pragma unroll
+            for (int d = 0; d < DH; ++d) dp[d & 3] += qs[qq][d] * ks[key][d];
+            const T dot = (dp[0] + dp[1]) + (dp[2] + dp[3]);
+            sc[i] = key < nk ? dot * (T)a.scale : (T)NEG_BIG;
+            cmax = cmax > sc[i] ? cmax : sc[i];
+        }
+#pragma unroll
+        for (int o2 = 1; o2 < 16; o2 <<= 1) {
+            const T other = __shfl_xor(cmax, o2);
+            cmax = cmax > other ? cmax : other;
+        }
+        const T m_new = m_run > cmax ? m_run : cmax;
+        const T alpha = exp_t<T>(m_run - m_new);
+        T psum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t key = kg + 16 * i;
+            const T p = key < nk ? exp_t<T>(sc[i] - m_new) : (T)0;
+            ps[qq][key] = p;
+            psum += p;
+        }
+#pragma unroll
+        for (int o2 = 1; o2 < 16; o2 <<= 1) psum += __shfl_xor(psum, o2);
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        __syncthreads();   // the query's probabilities (written by its 16 lanes)
+#pragma unroll
+        for (int d = 0; d < OD; ++d) o[d] *= alpha;
         for (uint32_t j = 0; j < nk; ++j) {
-            T dot = 0;
+            const T p = ps[qq][j];
 #pragma unroll
-            for (int d = 0; d < DP; ++d) dot += q[d] * ks[j][d0 + d];
-            dot += __shfl_xor(dot, 1);
-            dot += __shfl_xor(dot, 2);
-            const T sc = dot * (T)a.scale;
-            const T m_new = m_run > sc ? m_run : sc;
-            const T alpha = exp_t<T>(m_run - m_new), p = exp_t<T>(sc - m_new);
-            l_run = l_run * alpha + p;
-#pragma unroll
-            for (int d = 0; d < DP; ++d) o[d] = o[d] * alpha + p * (T)vs[j][d0 + d];
-            m_run = m_new;
+            for (int d = 0; d < OD; ++d) o[d] += p * (T)vs[j][od + d];
         }
     }
-    if (qi < a.S) {
+    if (q0 + qq < a.S) {
         const T inv = (T)1 / l_run;
 #pragma unroll
-        for (int d = 0; d < DP; d += 2)
-            *reinterpret_cast<float2*>(a.out + (size_t)qi * a.ldo + h * DH + d0 + d) =
+        for (int d = 0; d < OD; d += 2)
+            *reinterpret_cast<float2*>(a.out + (size_t)(q0 + qq) * a.ldo + h * DH + od + d) =
                 make_float2((float)(o[d] * inv), (float)(o[d + 1] * inv));
     }
 }
@@ -248,11 +281,11 @@ void attention_prefill_kernel(AttnPrefillArgs<T> a) {
 template <typename T>
 int launch_attention_prefill(const AttnPrefillArgs<T>& a, uint32_t dh, hipStream_t s) {
     if (a.S == 0) return MB_OK;
-    const dim3 grid(a.H, cdiv(a.S, QB)), block(256);
+    const dim3 grid(a.H, cdiv(a.S, QW)), block(256);
     switch (dh) {
-        case 32: hipLaunchKernelGGL((attention_prefill_kernel<8, T>), grid, block, 0, s, a); break;
-        case 64: hipLaunchKernelGGL((attention_prefill_kernel<16, T>), grid, block, 0, s, a); break;
-        case 128: hipLaunchKernelGGL((attention_prefill_kernel<32, T>), grid, block, 0, s, a); break;
+        case 32: hipLaunchKernelGGL((attention_prefill_kernel<32, T>), grid, block, 0, s, a); break;
+        case 64: hipLaunchKernelGGL((attention_prefill_kernel<64, T>), grid, block, 0, s, a); break;
+        case 128: hipLaunchKernelGGL((attention_prefill_kernel<128, T>), grid, block, 0, s, a); break;
         default: return fail(MB_E_ARG, "attention: head dim %u not 32, 64 or 128", dh);
     }
     MB_LAUNCH_CHECK("attention prefill");
@@ -341,7 +374,7 @@ int check_heads(uint32_t S, uint32_t D, uint32_t H, uint32_t HKV, uint32_t* dh) 
     *dh = D / H;
     if (*dh != 32 && *dh != 64 && *dh != 128)
         return fail(MB_E_ARG, "attention: head dim %u not 32, 64 or 128", *dh);
-    if (S > 65535u * QB) return fail(MB_E_ARG, "attention: S %u too large", S);
+    if (S > 65535u * QW) return fail(MB_E_ARG, "attention: S %u too large", S);
     return MB_OK;
 }
 
@@ -536,9 +569,9 @@ void register_transformer_f32() {
     register_kernel({"matvec_f32", run_matvec,
                      reinterpret_cast<const void*>(&matvec_kernel<true>), 1});
     register_kernel({"llama_attention_f32", run_llama_attention,
-                     reinterpret_cast<const void*>(&attention_prefill_kernel<8, float>), 1});
+                     reinterpret_cast<const void*>(&attention_prefill_kernel<32, float>), 1});
     register_kernel({"llama_decoder_layer_f32", run_llama_decoder_layer,
-                     reinterpret_cast<const void*>(&attention_prefill_kernel<8, double>), 5});
+                     reinterpret_cast<const void*>(&attention_prefill_kernel<32, double>), 5});
 }
 
 }  // namespace mb
