@@ -295,63 +295,87 @@ int launch_attention_prefill(const AttnPrefillArgs<T>& a, uint32_t dh, hipStream
 // ---- fp64 RMSNorm GEMM (the decoder layer's q|k|v projection) -----------------------------
 
 // C[S][N] = rmsnorm(A) B in fp64 from fp32 A [S][K] and B [K][N]: each
-// workgroup computes a 64 x 64 tile, thread (ty, tx) the 4 x 4 outputs of rows
-// 4 ty .. 4 ty + 3 and columns tx, tx + 16, tx + 32, tx + 48; A and B go
-// through LDS 32 k at a time, widened to fp64 on the way in.  The row scale
-// rsqrt(mean(a^2) + eps) is accumulated from the same A chunks.
-constexpr int G64 = 64, GK = 32;
+// workgroup computes a 32 x 64 tile, thread (ty, tx) the 2 x 4 outputs of rows
+// 2 ty, 2 ty + 1 and columns tx, tx + 16, tx + 32, tx + 48; A and B go
+// through LDS 32 k at a time, widened to fp64 on the way in, and the next
+// chunk's global loads are in flight while the current one is multiplied.
+// The row scale rsqrt(mean(a^2) + eps) is accumulated from the same A chunks.
+// (With 64 x 64 tiles and each chunk loaded only after the previous one was
+// multiplied, the decoder layer's 64 x 256 x 128 projection ran on 4
+// workgroups and took 23.8 us, four load round trips in a row.)
+constexpr int GR = 32, GC = 64, GK = 32;
 
 __global__ __launch_bounds__(256)
 void rms_gemm_f64_kernel(const float* __restrict__ A, const float* __restrict__ B,
                          double* __restrict__ C, uint32_t S, uint32_t N, uint32_t K, float eps) {
-    __shared__ double as[G64][GK + 1];
-    __shared__ double bs[GK][G64 + 1];
-    __shared__ double rs[G64];
+    __shared__ double as[GR][GK + 1];
+    __shared__ double bs[GK][GC + 1];
+    __shared__ double rs[GR];
     const uint32_t tid = threadIdx.x, tx = tid % 16, ty = tid / 16;
-    const uint32_t row0 = blockIdx.y * G64, col0 = blockIdx.x * G64;
-    double acc[4][4] = {};
-    double ss = 0;   // sum of squares of row row0 + tid / 4, quarter tid % 4 of each chunk
-    for (uint32_t k0 = 0; k0 < K; k0 += GK) {
-        __syncthreads();
-        for (uint32_t e = tid; e < G64 * GK; e += 256) {
-            const uint32_t r = e / GK, c = e % GK;
+    const uint32_t row0 = blockIdx.y * GR, col0 = blockIdx.x * GC;
+    constexpr int LA = GR * GK / 256, LB = GK * GC / 256;   // elements per thread per chunk
+    float ra[LA], rb[LB];
+    auto load = [&](uint32_t k0) {
+#pragma unroll
+        for (int i = 0; i < LA; ++i) {
+            const uint32_t e = tid + 256 * i, r = e / GK, c = e % GK;
             const uint32_t gr = row0 + r, gk = k0 + c;
-            as[r][c] = (gr < S && gk < K) ? (double)A[(size_t)gr * K + gk] : 0.0;
-            const uint32_t kr = e / G64, nc = e % G64;
-            bs[kr][nc] = (k0 + kr < K && col0 + nc < N) ? (double)B[(size_t)(k0 + kr) * N + col0 + nc]
-                                                        : 0.0;
+            ra[i] = (gr < S && gk < K) ? A[(size_t)gr * K + gk] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < LB; ++i) {
+            const uint32_t e = tid + 256 * i, kr = e / GC, nc = e % GC;
+            rb[i] = (k0 + kr < K && col0 + nc < N) ? B[(size_t)(k0 + kr) * N + col0 + nc] : 0.f;
+        }
+    };
+    double acc[2][4] = {};
+    double ss = 0;   // sum of squares of row tid / 8, k quarter (tid % 8) * 4 of each chunk
+    load(0);
+    for (uint32_t k0 = 0; k0 < K; k0 += GK) {
+        __syncthreads();   // the previous chunk is no longer read
+#pragma unroll
+        for (int i = 0; i < LA; ++i) {
+            const uint32_t e = tid + 256 * i;
+            as[e / GK][e % GK] = (double)ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < LB; ++i) {
+            const uint32_t e = tid + 256 * i;
+            bs[e / GC][e % GC] = (double)rb[i];
         }
         __syncthreads();
+        if (k0 + GK < K) load(k0 + GK);
 #pragma unroll
-        for (int c = 0; c < GK / 4; ++c) {
-            const double v = as[tid / 4][(tid % 4) * (GK / 4) + c];
+        for (int c = 0; c < 4; ++c) {
+            const double v = as[tid / 8][(tid % 8) * 4 + c];
             ss += v * v;
         }
 #pragma unroll 4
         for (int kk = 0; kk < GK; ++kk) {
-            double av[4], bv[4];
+            double av[2], bv[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) av[i] = as[4 * ty + i][kk];
+            for (int i = 0; i < 2; ++i) av[i] = as[2 * ty + i][kk];
 #pragma unroll
             for (int j = 0; j < 4; ++j) bv[j] = bs[kk][tx + 16 * j];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[i][j] += av[i] * bv[j];
         }
     }
     ss += __shfl_xor(ss, 1);
     ss += __shfl_xor(ss, 2);
-    if (tid % 4 == 0) rs[tid / 4] = 1.0 / sqrt(ss / (double)K + (double)eps);
+    ss += __shfl_xor(ss, 4);
+    if (tid % 8 == 0) rs[tid / 8] = 1.0 / sqrt(ss / (double)K + (double)eps);
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t r = row0 + 4 * ty + i;
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t r = row0 + 2 * ty + i;
         if (r >= S) continue;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t c = col0 + tx + 16 * j;
-            if (c < N) C[(size_t)r * N + c] = acc[i][j] * rs[4 * ty + i];
+            if (c < N) C[(size_t)r * N + c] = acc[i][j] * rs[2 * ty + i];
         }
     }
 }
@@ -360,7 +384,7 @@ int launch_rms_gemm_f64(const float* a, const float* b, double* c, uint32_t S, u
                         uint32_t K, float eps, hipStream_t s) {
     if (S == 0 || N == 0) return MB_OK;
     if (K == 0) return fail(MB_E_ARG, "rms gemm: K must be positive");
-    hipLaunchKernelGGL(rms_gemm_f64_kernel, dim3(cdiv(N, G64), cdiv(S, G64)), dim3(256), 0, s,
+    hipLaunchKernelGGL(rms_gemm_f64_kernel, dim3(cdiv(N, GC), cdiv(S, GR)), dim3(256), 0, s,
                        a, b, c, S, N, K, eps);
     MB_LAUNCH_CHECK("rms_gemm_f64");
     return MB_OK;
