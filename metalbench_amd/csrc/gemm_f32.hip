@@ -758,18 +758,21 @@ void register_gemm_f32() {
     const void* plain = reinterpret_cast<const void*>(
         &gemm_f32_kernel<2, true, BL_KN, EPI_STORE, false>);
     // sqr_mm, rect_mm and fused_qkv_projection share the plain GEMM's spec;
-    // their registry shapes run the LDS-DMA kernel, whose attributes (LDS
-    // size, threads) the report prints.
+    // the attributes (LDS size, threads) the report prints are those of the
+    // kernel each registry shape runs: the LDS-DMA kernel for sqr_mm and
+    // rect_mm, the small-problem kernel for fused_qkv_projection (and swiglu).
     const void* dma = reinterpret_cast<const void*>(&gemm_f32_dma_kernel<BL_KN, false>);
     register_kernel({"sqr_matmul_f32", run_gemm_f32, dma, 1});
     register_kernel({"rect_matmul_f32", run_gemm_f32, dma, 1});
-    register_kernel({"fused_qkv_projection_f32", run_gemm_f32, dma, 1});
+    register_kernel({"fused_qkv_projection_f32", run_gemm_f32,
+                     reinterpret_cast<const void*>(&gemm_f32_small_kernel<BL_KN, EPI_STORE, false>),
+                     1});
     register_kernel({"batch_matmul_f32", run_batch_mm, plain, 1});
     // (rms_norm_linear's registry shape, 1024^3, takes the LDS-DMA kernel)
     register_kernel({"rms_norm_linear_f32", run_rms_norm_linear,
                      reinterpret_cast<const void*>(&gemm_f32_dma_kernel<BL_NK, true>), 1});
     register_kernel({"swiglu_f32", run_swiglu,
-                     reinterpret_cast<const void*>(&gemm_f32_kernel<2, true, BL_KN, EPI_SWIGLU, false>),
+                     reinterpret_cast<const void*>(&gemm_f32_small_kernel<BL_KN, EPI_SWIGLU, false>),
                      1});
 }
 
