@@ -295,19 +295,22 @@ int launch_attention_prefill(const AttnPrefillArgs<T>& a, uint32_t dh, hipStream
 // ---- fp64 RMSNorm GEMM (the decoder layer's q|k|v projection) -----------------------------
 
 // C[S][N] = rmsnorm(A) B in fp64 from fp32 A [S][K] and B [K][N]: each
-// workgroup computes a 32 x 64 tile, thread (ty, tx) the 2 x 4 outputs of rows
-// 2 ty, 2 ty + 1 and columns tx, tx + 16, tx + 32, tx + 48; A and B go
+// workgroup computes a (16 TR) x (16 TC) tile, thread (ty, tx) the TR x TC
+// outputs of rows TR ty .. TR ty + TR - 1 and columns tx + 16 j; A and B go
 // through LDS 32 k at a time, widened to fp64 on the way in, and the next
 // chunk's global loads are in flight while the current one is multiplied.
 // The row scale rsqrt(mean(a^2) + eps) is accumulated from the same A chunks.
 // (With 64 x 64 tiles and each chunk loaded only after the previous one was
 // multiplied, the decoder layer's 64 x 256 x 128 projection ran on 4
 // workgroups and took 23.8 us, four load round trips in a row.)
-constexpr int GR = 32, GC = 64, GK = 32;
+constexpr int GK = 32;
 
+template <int TR, int TC>   // rows and columns per thread: a (16 TR) x (16 TC) tile
 __global__ __launch_bounds__(256)
 void rms_gemm_f64_kernel(const float* __restrict__ A, const float* __restrict__ B,
                          double* __restrict__ C, uint32_t S, uint32_t N, uint32_t K, float eps) {
+    constexpr int GR = 16 * TR, GC = 16 * TC;
+    constexpr int RT = 256 / GR;      // threads per row for the sums of squares
     __shared__ double as[GR][GK + 1];
     __shared__ double bs[GK][GC + 1];
     __shared__ double rs[GR];
@@ -328,8 +331,8 @@ void rms_gemm_f64_kernel(const float* __restrict__ A, const float* __restrict__ 
             rb[i] = (k0 + kr < K && col0 + nc < N) ? B[(size_t)(k0 + kr) * N + col0 + nc] : 0.f;
         }
     };
-    double acc[2][4] = {};
-    double ss = 0;   // sum of squares of row tid / 8, k quarter (tid % 8) * 4 of each chunk
+    double acc[TR][TC] = {};
+    double ss = 0;   // sum of squares of row tid / RT, k part (tid % RT) of each chunk
     load(0);
     for (uint32_t k0 = 0; k0 < K; k0 += GK) {
         __syncthreads();   // the previous chunk is no longer read
@@ -346,36 +349,35 @@ void rms_gemm_f64_kernel(const float* __restrict__ A, const float* __restrict__ 
         __syncthreads();
         if (k0 + GK < K) load(k0 + GK);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const double v = as[tid / 8][(tid % 8) * 4 + c];
+        for (int c = 0; c < GK / RT; ++c) {
+            const double v = as[tid / RT][(tid % RT) * (GK / RT) + c];
             ss += v * v;
         }
 #pragma unroll 4
         for (int kk = 0; kk < GK; ++kk) {
-            double av[2], bv[4];
+            double av[TR], bv[TC];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) av[i] = as[2 * ty + i][kk];
+            for (int i = 0; i < TR; ++i) av[i] = as[TR * ty + i][kk];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) bv[j] = bs[kk][tx + 16 * j];
+            for (int j = 0; j < TC; ++j) bv[j] = bs[kk][tx + 16 * j];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TR; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] += av[i] * bv[j];
+                for (int j = 0; j < TC; ++j) acc[i][j] += av[i] * bv[j];
         }
     }
-    ss += __shfl_xor(ss, 1);
-    ss += __shfl_xor(ss, 2);
-    ss += __shfl_xor(ss, 4);
-    if (tid % 8 == 0) rs[tid / 8] = 1.0 / sqrt(ss / (double)K + (double)eps);
+#pragma unroll
+    for (int o2 = 1; o2 < RT; o2 <<= 1) ss += __shfl_xor(ss, o2);
+    if (tid % RT == 0) rs[tid / RT] = 1.0 / sqrt(ss / (double)K + (double)eps);
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const uint32_t r = row0 + 2 * ty + i;
+    for (int i = 0; i < TR; ++i) {
+        const uint32_t r = row0 + TR * ty + i;
         if (r >= S) continue;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < TC; ++j) {
             const uint32_t c = col0 + tx + 16 * j;
-            if (c < N) C[(size_t)r * N + c] = acc[i][j] * rs[2 * ty + i];
+            if (c < N) C[(size_t)r * N + c] = acc[i][j] * rs[TR * ty + i];
         }
     }
 }
@@ -384,8 +386,10 @@ int launch_rms_gemm_f64(const float* a, const float* b, double* c, uint32_t S, u
                         uint32_t K, float eps, hipStream_t s) {
     if (S == 0 || N == 0) return MB_OK;
     if (K == 0) return fail(MB_E_ARG, "rms gemm: K must be positive");
-    hipLaunchKernelGGL(rms_gemm_f64_kernel, dim3(cdiv(N, GC), cdiv(S, GR)), dim3(256), 0, s,
-                       a, b, c, S, N, K, eps);
+    // 16 x 32 tiles: 32 workgroups at the registry's 64 x 256 (34 us for the
+    // layer, against 35-36 us with 32 x 32 or 32 x 64 tiles and 16 x 64)
+    hipLaunchKernelGGL((rms_gemm_f64_kernel<1, 2>), dim3(cdiv(N, 32), cdiv(S, 16)), dim3(256), 0,
+                       s, a, b, c, S, N, K, eps);
     MB_LAUNCH_CHECK("rms_gemm_f64");
     return MB_OK;
 }
