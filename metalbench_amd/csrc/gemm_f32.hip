@@ -438,36 +438,42 @@ void gemm_f32_dma_kernel(GemmF32Args g) {
     stage(I3{}, I4{}, nstages - 1);
     __syncthreads();
 
-    // The second K half hands its partial sums to the first through LDS.
+    // The two K halves of each 32 x 32 block finish half of it each.  In the
+    // 32x32 accumulator layout (lane l, register r -> row 8 (r / 4) +
+    // 4 (l / 32) + r % 4, column l % 32) registers 0-7 hold rows 0-15 and
+    // registers 8-15 rows 16-31: the wk = 0 wave keeps 0-7 and hands 8-15 to
+    // its partner through LDS, the wk = 1 wave keeps 8-15 and hands 0-7.
+    // Each adds the partner's partial to its own (a + b == b + a exactly, so
+    // the sum does not depend on which wave adds) and stores its 16 rows; C
+    // is written once and not read here: non-temporal stores.
     float* red = &L[0][0];
-    if (wk == 1) {
+    float* mine = red + ((wave & 3) * 2 + wk) * 8 * 64;
+    const float* theirs = red + ((wave & 3) * 2 + (wk ^ 1)) * 8 * 64;
+    if (wk == 0) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) red[((wave & 3) * 16 + r) * 64 + lane] = acc[r];
+        for (int r = 0; r < 8; ++r) mine[r * 64 + lane] = acc[8 + r];
+    } else {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) mine[r * 64 + lane] = acc[r];
     }
     if (RMS) {   // lanes li and li + 32 read row wm*32 + li's two chunks of each group
         ss += __shfl_xor(ss, 32);
         if (wn == 0 && lh == 0) row_ss[wk][wm * 32 + li] = ss;
     }
     __syncthreads();
-    if (wk == 1) return;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] += red[((wave & 3) * 16 + r) * 64 + lane];
-    if (RMS) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const uint32_t lr = wm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-            acc[r] *= rsqrtf((row_ss[0][lr] + row_ss[1][lr]) / (float)K + g.eps);
-        }
-    }
-
-    // 32x32 accumulator layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
-    // C is written once and not read here: non-temporal stores.
     const uint32_t gc = n0 + wn * 32 + li;
+    auto finish = [&](auto base_c) {
+        constexpr int R0 = decltype(base_c)::value;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const uint32_t gr = m0 + wm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        __builtin_nontemporal_store(acc[r], &C[(size_t)gr * g.ldc + gc]);
-    }
+        for (int r = 0; r < 8; ++r) {
+            float v = acc[R0 + r] + theirs[r * 64 + lane];
+            const uint32_t lr = wm * 32 + 8 * ((R0 + r) >> 2) + 4 * lh + (r & 3);
+            if (RMS) v *= rsqrtf((row_ss[0][lr] + row_ss[1][lr]) / (float)K + g.eps);
+            __builtin_nontemporal_store(v, &C[(size_t)(m0 + lr) * g.ldc + gc]);
+        }
+    };
+    if (wk == 0) finish(std::integral_constant<int, 0>{});
+    else finish(std::integral_constant<int, 8>{});
 }
 
 // Small problems (fewer 64 x 64 tiles than half the CUs, K <= 512: the
