@@ -372,18 +372,25 @@ void conv2d_f32_dma_kernel(const float* __restrict__ X, const float* __restrict_
     __builtin_amdgcn_s_waitcnt(0);   // no DMA may still target LDS
     lds_barrier();
 
-    float* red = L;   // NW/2 waves x 16 x 64 floats
+    // The two K halves of each 32 x 32 block finish half of it each.  In the
+    // 32x32 accumulator layout (lane l, reg r -> row 8 (r / 4) + 4 (l / 32) +
+    // r % 4, col l % 32) registers 0-7 hold rows 0-15 and registers 8-15 rows
+    // 16-31: the wk = 0 wave keeps 0-7 and hands 8-15 to its partner through
+    // LDS, the wk = 1 wave keeps 8-15 and hands 0-7.  Each adds the partner's
+    // partial to its own (a + b == b + a exactly) and stores its 16 rows, so
+    // each wave issues half the epilogue's LDS accesses and stores.
     const uint32_t rw = wave % (NW / 2);
-    if (wk == 1) {
+    float* mine = L + (rw * 2 + wk) * 8 * 64;   // NW waves x 8 x 64 floats
+    const float* theirs = L + (rw * 2 + (wk ^ 1)) * 8 * 64;
+    if (wk == 0) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) red[(rw * 16 + r) * 64 + lane] = acc[r];
+        for (int r = 0; r < 8; ++r) mine[r * 64 + lane] = acc[8 + r];
+    } else {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) mine[r * 64 + lane] = acc[r];
     }
     __syncthreads();
-    if (wk == 1) return;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] += red[(rw * 16 + r) * 64 + lane];
 
-    // 32x32 accumulator: lane l, reg r -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
     // Buffer stores through a descriptor clipped to the output: rows past M
     // fall outside it, columns past O take an out-of-range offset.  One
     // 32-bit add per store instead of a guarded 64-bit address: this
@@ -395,11 +402,17 @@ void conv2d_f32_dma_kernel(const float* __restrict__ X, const float* __restrict_
         Y, 0, __builtin_amdgcn_readfirstlane(sh.m * sh.o * 4), 0x00020000);
     const uint32_t ybase = gc < sh.o ? ((m0 + wm * 32 + 4 * lh) * sh.o + gc) * 4 : 0x80000000u;
     const uint32_t o4 = sh.o * 4;
+    auto finish = [&](auto base_c) {
+        constexpr int R0 = decltype(base_c)::value;
 #pragma unroll
-    for (int r = 0; r < 16; ++r)   // (not __builtin_bit_cast(uint32_t, acc[r]): hipcc
-                                   // compiled that as a read of element 0)
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[r]), yrs,
-                                              ybase + (8 * (r >> 2) + (r & 3)) * o4, 0, 0);
+        for (int r = 0; r < 8; ++r) {
+            const float v = acc[R0 + r] + theirs[r * 64 + lane];
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yrs,
+                                                  ybase + (8 * ((R0 + r) >> 2) + (r & 3)) * o4, 0, 0);
+        }
+    };
+    if (wk == 0) finish(std::integral_constant<int, 0>{});
+    else finish(std::integral_constant<int, 8>{});
 }
 
 int launch_conv2d(const float* x, const float* w, float* y, uint32_t n, uint32_t h, uint32_t wd,
